@@ -1,0 +1,210 @@
+"""Benchmark: GSA layer forward tokens/s on one MI355X, with the sparse-attention
+roofline and the CPU oracle timed beside it.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--cpu-seconds S]
+
+One step = one GatedSparseAttention forward over one batch of synthetic input
+already resident in HBM (fused projection GEMM, fused indexer + exact top-k,
+RoPE/gate producer, sparse gather-attention with the output gate, o_proj).
+Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GSA fwd tokens/sec @T=16384 bf16, 1 MI355X; indexer MFMA% + attn HBM GB/s%"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+# (B, T) per config; every config: D=2048, H=16, d=128, H_idx=4, d_idx=64, k_base=2048, k_max=4096
+CONFIGS = {"c2": (1, 4096), "c3": (1, 16384), "c4": (4, 8192), "c5": (1, 65536)}
+D, H, DH, HI, DI = 2048, 16, 128, 4, 64
+K_BASE, K_MIN, K_MAX = 2048, 256, 4096
+
+
+def synthetic_model(dev, dtype, seed=0):
+    """Random-init GSA layer: weights N(0, 0.02), gate biases 0.5, indexer biases 0."""
+    from gsa_gdn_benchmarkstudy_amd import GatedSparseAttention
+
+    m = GatedSparseAttention(D, H, k_max=K_MAX, d_indexer=DI, n_idx_heads=HI, k_base=K_BASE, k_min=K_MIN)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if name.endswith("gate_proj.bias"):
+                p.fill_(0.5)
+            elif name.endswith("bias"):
+                p.zero_()
+            else:
+                p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+    m = m.to(dev).to(dtype).eval()
+    m.fuse_projections()
+    return m
+
+
+def attn_bytes(B, T, k_eff, s=2):
+    """Algorithmic bytes of one sparse-attention launch: gathered K+V rows of the
+    valid selected entries, their int32 indices, the q read and out write, and
+    the output-gate logits."""
+    P = B * sum(min(t + 1, k_eff) for t in range(T))
+    return P * H * DH * 2 * s + 4 * P + 2 * B * T * H * DH * s + B * T * D * s, P
+
+
+def indexer_flops(B, T):
+    """Causal indexer MACs x2: every (i, j <= i) pair, 4 heads of 64."""
+    return 2 * B * HI * DI * T * (T + 1) // 2
+
+
+def cpu_baseline(B, T, budget_s, dtype=torch.bfloat16):
+    """The CPU oracle (restatement of gsa_ref.py's forward) on sampled query rows
+    of the same workload: per-token cost = the token's own projections plus its
+    indexer row, selection, gathered attention and o_proj, over row chunks spread
+    evenly across the sequence, until the time budget is spent."""
+    from oracle import gsa_oracle as orc
+
+    ncores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(ncores)
+    cfg = orc.GSAConfig(hidden_size=D, num_heads=H, k_max=K_MAX, d_indexer=DI, n_idx_heads=HI,
+                        k_base=K_BASE, k_min=K_MIN)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=0), dtype)
+    x = orc.synthetic_input(B, T, D, seed=1).to(dtype)
+    chunk = 32
+    with torch.inference_mode():
+        p_all = orc.project(sd, cfg, x)                 # untimed: keys/values of every row
+        starts = [int(i * (T - chunk) / 63) for i in range(64)]
+        # order the chunks so any prefix is spread over the sequence
+        order = sorted(range(64), key=lambda i: int(format(i, "06b")[::-1], 2))
+        done_rows, spent = 0, 0.0
+        orc.attend_rows(sd, cfg, p_all, starts[0], starts[0] + chunk)   # warm-up
+        for i in order:
+            r0 = starts[i]
+            t0 = time.perf_counter()
+            orc.project(sd, cfg, x[:, r0:r0 + chunk])
+            orc.attend_rows(sd, cfg, p_all, r0, r0 + chunk)
+            spent += time.perf_counter() - t0
+            done_rows += chunk
+            if spent >= budget_s:
+                break
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": B * done_rows / spent, "unit": "tokens/s", "cores": ncores, "kind": "port",
+        "sample": (f"CPU oracle (torch restatement of gsa_ref.py forward, {str(dtype).split('.')[-1]}) "
+                   f"on {done_rows} of {T} query rows in {done_rows // chunk} chunks of {chunk} spread "
+                   f"over the sequence; per row: its 8 projections + indexer row vs all keys + top-k "
+                   f"+ gathered attention + gate + o_proj; keys/values of all rows precomputed untimed; "
+                   f"{spent:.1f} s timed; {cpu_model}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="c3")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build runs the "
+              f"GSA forward on a single MI355X; multi-GPU sharding is design-only)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+
+    dev = torch.device("cuda:0")
+    B, T = CONFIGS[args.config]
+    dtype = torch.bfloat16
+    model = synthetic_model(dev, dtype)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    x = torch.randn(B, T, D, generator=g)
+    if args.config == "c4":   # per-sequence sigma ~ U(0.5, 2)
+        x = x * (0.5 + 1.5 * torch.rand(B, generator=g)).view(B, 1, 1)
+    x = x.to(dtype).to(dev)
+    k_eff = model.topk_selector.k_effective(T)
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model(x)
+        torch.cuda.synchronize()
+        model.attn_events = []
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            model(x)
+        end.record()
+        torch.cuda.synchronize()
+        evs = model.attn_events
+        model.attn_events = None
+    total_ms = start.elapsed_time(end)
+    ms = total_ms / args.steps
+    attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+
+    # indexer kernel alone (same stream discipline, timed separately)
+    with torch.no_grad():
+        views = model.project(x)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        n_idx = 5
+        for _ in range(n_idx):
+            model.select(views, T)
+        e1.record()
+        torch.cuda.synchronize()
+        idx_ms = e0.elapsed_time(e1) / n_idx
+        del views
+
+    abytes, P = attn_bytes(B, T, k_eff)
+    achieved = abytes / (attn_ms * 1e-3) / 1e9
+    fidx = indexer_flops(B, T)
+    idx_tflops = fidx / (idx_ms * 1e-3) / 1e12
+
+    out = {
+        "metric": METRIC,
+        "value": B * T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: x~N(0,1) (c4: per-sequence sigma~U(0.5,2)), weights~N(0,0.02), gate biases 0.5, "
+                "indexer biases 0, random init",
+        "config": {"workload": f"GSA layer forward B={B} T={T} D={D} H={H} d={DH} H_idx={HI} d_idx={DI} "
+                               f"k_eff={k_eff} causal", "name": args.config, "batch": B, "seq_len": T,
+                   "k_eff": k_eff},
+        "roofline": {"kernel": "gsa_sparse_attn", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": abytes, "valid_pairs": P, "ms": attn_ms},
+        "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,
+                    "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": idx_tflops / BF16_PEAK_TFLOPS,
+                    "flops": fidx, "ms": idx_ms},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(B, T, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

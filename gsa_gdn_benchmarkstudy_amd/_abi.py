@@ -1,0 +1,275 @@
+"""ctypes binding of libgsa_hip.so (C ABI declared in include/gsa_hip.h).
+
+The library is loaded after ``torch`` so that both share torch's HIP runtime
+(one device context, one set of streams).  Every wrapper takes torch tensors,
+checks their layout, passes raw pointers, strides and the current HIP stream,
+and turns a non-zero status into ``RuntimeError``.  There is no fallback: a
+missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgsa_hip.so")
+
+ABI_VERSION = 1
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+ORDER_INDEX_ASC = 0
+ORDER_SCORE_DESC = 1
+TOPK_DESC_MAX_K = 4096
+
+ATTN_ROPE_Q = 1
+ATTN_OUT_GATE = 2
+
+# Every symbol include/gsa_hip.h declares.
+EXPORTS = (
+    "gsa_abi_version", "gsa_status_string", "gsa_indexer_scores", "gsa_topk_select",
+    "gsa_indexer_select", "gsa_prologue", "gsa_sparse_attn",
+)
+
+_vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+
+_PROTOS = {
+    "gsa_abi_version": ([], _i32),
+    "gsa_status_string": ([_i32], ctypes.c_char_p),
+    "gsa_indexer_scores": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
+                            _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp], _i32),
+    "gsa_topk_select": ([_vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
+    "gsa_indexer_select": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
+                            _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
+    "gsa_prologue": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
+                      _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
+    "gsa_sparse_attn": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
+                         _vp, _i64, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
+                         _vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp], _i32),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libgsa_hip.so once; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m gsa_gdn_benchmarkstudy_amd.build`")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (args, res) in _PROTOS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    if lib.gsa_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"libgsa_hip.so ABI {lib.gsa_abi_version()} != {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def status_string(status: int) -> str:
+    return load().gsa_status_string(status).decode()
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed: status {status} ({status_string(status)})")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return DTYPE_BF16
+    if dt == torch.float32:
+        return DTYPE_F32
+    raise TypeError(f"unsupported dtype {dt}: the HIP kernels take bfloat16 or float32")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need_cuda(*ts: Optional[torch.Tensor]) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("the HIP kernels need device tensors (got a CPU tensor)")
+
+
+def _expect(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _rows(t: torch.Tensor, inner: int):
+    """(batch stride, row stride) of a [B, T, ...] tensor whose trailing ``inner``
+    elements per row are contiguous."""
+    flat = 1
+    for d in range(t.dim() - 1, 1, -1):
+        if t.stride(d) != flat:
+            raise ValueError(f"tensor {tuple(t.shape)} strides {t.stride()}: inner dims must be contiguous")
+        flat *= t.shape[d]
+    if flat != inner:
+        raise ValueError(f"tensor {tuple(t.shape)}: expected {inner} elements per row")
+    return t.stride(0), t.stride(1)
+
+
+# ---------------------------------------------------------------------------
+# Wrappers
+# ---------------------------------------------------------------------------
+
+def indexer_scores(q_idx, k_idx, w, bias32, scale: float, causal: bool = True,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp32 [B,T,T] scores; q_idx [B,T,Hi,di], k_idx [B,T,di], w [B,T,Hi], bias32 fp32 [Hi]."""
+    lib = load()
+    _need_cuda(q_idx, k_idx, w, bias32)
+    B, T, Hi, di = q_idx.shape
+    _expect(tuple(k_idx.shape) == (B, T, di), f"k_idx {tuple(k_idx.shape)} != {(B, T, di)}")
+    _expect(tuple(w.shape) == (B, T, Hi), f"w {tuple(w.shape)} != {(B, T, Hi)}")
+    _expect(bias32.dtype == torch.float32 and bias32.numel() == Hi and bias32.is_contiguous(), "bias: fp32 [Hi]")
+    _expect(k_idx.dtype == q_idx.dtype == w.dtype, "q_idx, k_idx, w must share a dtype")
+    if out is None:
+        out = torch.empty(B, T, T, device=q_idx.device, dtype=torch.float32)
+    _expect(tuple(out.shape) == (B, T, T) and out.dtype == torch.float32, "out: fp32 [B,T,T]")
+    qs, ks, ws, os_ = _rows(q_idx, Hi * di), _rows(k_idx, di), _rows(w, Hi), _rows(out, T)
+    st = lib.gsa_indexer_scores(_ptr(q_idx), *qs, _ptr(k_idx), *ks, _ptr(w), *ws,
+                                _ptr(bias32), float(scale), B, T, Hi, di, int(bool(causal)),
+                                dtype_code(q_idx.dtype), _ptr(out), *os_, _stream(q_idx))
+    _check(st, "gsa_indexer_scores")
+    return out
+
+
+def topk_select(scores: torch.Tensor, k_eff: int, order: int = ORDER_INDEX_ASC,
+                want_mask: bool = False):
+    """Exact per-row top-k of fp32 scores [B,T,Tkv] -> (idx int32, count int32, mask uint8|None)."""
+    lib = load()
+    _need_cuda(scores)
+    if scores.dtype != torch.float32:
+        raise TypeError("scores must be float32")
+    _expect(scores.dim() == 3, "scores: [B,T,Tkv]")
+    B, T, Tkv = scores.shape
+    if scores.stride(2) != 1:
+        raise ValueError("scores must have unit column stride")
+    idx = torch.empty(B, T, k_eff, device=scores.device, dtype=torch.int32)
+    cnt = torch.empty(B, T, device=scores.device, dtype=torch.int32)
+    mask = torch.empty(B, T, k_eff, device=scores.device, dtype=torch.uint8) if want_mask else None
+    st = lib.gsa_topk_select(_ptr(scores), scores.stride(0), scores.stride(1), B, T, Tkv, int(k_eff),
+                             int(order), _ptr(idx), _ptr(cnt), _ptr(mask), _stream(scores))
+    _check(st, "gsa_topk_select")
+    return idx, cnt, mask
+
+
+def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int,
+                   idx: Optional[torch.Tensor] = None, cnt: Optional[torch.Tensor] = None):
+    """Fused indexer + top-k -> (idx int32 [B,T,k_eff] ascending, count int32 [B,T])."""
+    lib = load()
+    _need_cuda(q_idx, k_idx, w, bias32)
+    B, T, Hi, di = q_idx.shape
+    _expect(tuple(k_idx.shape) == (B, T, di), f"k_idx {tuple(k_idx.shape)} != {(B, T, di)}")
+    _expect(tuple(w.shape) == (B, T, Hi), f"w {tuple(w.shape)} != {(B, T, Hi)}")
+    _expect(bias32.dtype == torch.float32 and bias32.numel() == Hi and bias32.is_contiguous(), "bias: fp32 [Hi]")
+    _expect(k_idx.dtype == q_idx.dtype == w.dtype, "q_idx, k_idx, w must share a dtype")
+    if idx is None:
+        idx = torch.empty(B, T, k_eff, device=q_idx.device, dtype=torch.int32)
+    if cnt is None:
+        cnt = torch.empty(B, T, device=q_idx.device, dtype=torch.int32)
+    _expect(tuple(idx.shape) == (B, T, k_eff) and idx.dtype == torch.int32 and idx.is_contiguous(),
+            "idx: contiguous int32 [B,T,k_eff]")
+    _expect(tuple(cnt.shape) == (B, T) and cnt.dtype == torch.int32 and cnt.is_contiguous(),
+            "count: contiguous int32 [B,T]")
+    qs, ks, ws = _rows(q_idx, Hi * di), _rows(k_idx, di), _rows(w, Hi)
+    st = lib.gsa_indexer_select(_ptr(q_idx), *qs, _ptr(k_idx), *ks, _ptr(w), *ws, _ptr(bias32),
+                                float(scale), B, T, Hi, di, int(k_eff), dtype_code(q_idx.dtype),
+                                _ptr(idx), _ptr(cnt), _stream(q_idx))
+    _check(st, "gsa_indexer_select")
+    return idx, cnt
+
+
+def prologue(k=None, v=None, vg=None, cos=None, sin=None, k_out=None, v_out=None):
+    """RoPE(k) -> k_out and/or v*sigmoid(vg) -> v_out; tensors [B,T,H,d], cos/sin [T,d]."""
+    lib = load()
+    ref = k if k is not None else v
+    _need_cuda(k, v, vg, cos, sin)
+    B, T, H, d = ref.shape
+    HD = H * d
+    for t, nm in ((k, "k"), (v, "v"), (vg, "vg"), (k_out, "k_out"), (v_out, "v_out")):
+        if t is not None:
+            _expect(tuple(t.shape) == (B, T, H, d) and t.dtype == ref.dtype, f"{nm}: {ref.dtype} [B,T,H,d]")
+    if k is not None:
+        _expect(cos is not None and sin is not None, "RoPE needs cos and sin")
+        _expect(cos.dim() == 2 and cos.shape[0] >= T and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape)
+                and cos.dtype == sin.dtype == ref.dtype, "cos/sin: [>=T, d] in the tensor dtype")
+    if v is not None:
+        _expect(vg is not None, "the gate needs its logits")
+    if k is not None and k_out is None:
+        k_out = torch.empty(B, T, H, d, device=ref.device, dtype=ref.dtype)
+    if v is not None and v_out is None:
+        v_out = torch.empty(B, T, H, d, device=ref.device, dtype=ref.dtype)
+    ks = _rows(k, HD) if k is not None else (0, 0)
+    vs = _rows(v, HD) if v is not None else (0, 0)
+    gs = _rows(vg, HD) if vg is not None else (0, 0)
+    cs = cos.stride(0) if cos is not None else 0
+    if cos is not None and (cos.stride(-1) != 1 or sin.stride(0) != cs or sin.stride(-1) != 1):
+        raise ValueError("cos/sin must be [T, d] with unit element stride and equal row strides")
+    for t in (k_out, v_out):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("outputs must be contiguous")
+    st = lib.gsa_prologue(_ptr(k), *ks, _ptr(v), *vs, _ptr(vg), *gs, _ptr(cos), _ptr(sin), cs,
+                          B, T, H, d, dtype_code(ref.dtype), _ptr(k_out), _ptr(v_out), _stream(ref))
+    _check(st, "gsa_prologue")
+    return k_out, v_out
+
+
+def sparse_attn(q, k, v, idx, scale: float, count=None, mask=None, og=None, cos=None, sin=None,
+                flags: int = 0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Gather attention -> out [B,T,H,d]; idx int32 [B,T,k_sel] (mask uint8 with the same strides)."""
+    lib = load()
+    _need_cuda(q, k, v, idx, count, mask, og, cos, sin)
+    B, T, H, d = q.shape
+    Tkv = k.shape[1]
+    HD = H * d
+    _expect(k.shape[0] == B and tuple(k.shape[2:]) == (H, d) and tuple(v.shape) == tuple(k.shape),
+            "k, v: [B,Tkv,H,d] matching q")
+    _expect(k.dtype == v.dtype == q.dtype, "q, k, v must share a dtype")
+    _expect(idx.dim() == 3 and tuple(idx.shape[:2]) == (B, T), "idx: [B,T,k_sel]")
+    if mask is not None:
+        _expect(tuple(mask.shape) == tuple(idx.shape), "mask: idx's shape")
+    if count is not None:
+        _expect(tuple(count.shape) == (B, T), "count: [B,T]")
+    if og is not None:
+        _expect(tuple(og.shape) == (B, T, H, d) and og.dtype == q.dtype, "og: [B,T,H,d] in q's dtype")
+    if flags & ATTN_ROPE_Q:
+        _expect(cos is not None and sin is not None and cos.dim() == 2 and cos.shape[0] >= T
+                and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape)
+                and cos.dtype == sin.dtype == q.dtype and cos.stride(1) == 1 and sin.stride() == cos.stride(),
+                "cos/sin: [>=T, d] in q's dtype")
+    if out is not None:
+        _expect(tuple(out.shape) == (B, T, H, d) and out.dtype == q.dtype, "out: [B,T,H,d] in q's dtype")
+    if idx.dtype != torch.int32 or (count is not None and count.dtype != torch.int32):
+        raise TypeError("idx and count must be int32")
+    if idx.stride(2) != 1:
+        raise ValueError("idx must have unit stride along k")
+    if mask is not None and (mask.dtype not in (torch.uint8, torch.bool) or mask.stride() != idx.stride()):
+        raise ValueError("mask must be uint8/bool with idx's strides")
+    if count is not None and not count.is_contiguous():
+        raise ValueError("count must be contiguous [B,T]")
+    if out is None:
+        out = torch.empty(B, T, H, d, device=q.device, dtype=q.dtype)
+    os_ = _rows(og, HD) if og is not None else (0, 0)
+    cs = cos.stride(0) if cos is not None else 0
+    st = lib.gsa_sparse_attn(_ptr(q), *_rows(q, HD), _ptr(k), *_rows(k, HD), _ptr(v), *_rows(v, HD),
+                             _ptr(idx), idx.stride(0), idx.stride(1), idx.shape[2],
+                             _ptr(count), _ptr(mask), _ptr(og), *os_, _ptr(cos), _ptr(sin), cs,
+                             _ptr(out), *_rows(out, HD), B, T, Tkv, H, d, float(scale),
+                             dtype_code(q.dtype), int(flags), _stream(q))
+    _check(st, "gsa_sparse_attn")
+    return out

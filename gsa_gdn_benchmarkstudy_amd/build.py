@@ -1,0 +1,74 @@
+"""Build libgsa_hip.so (the gfx950 kernels and their C ABI) in-tree with hipcc.
+
+Usage: ``python -m gsa_gdn_benchmarkstudy_amd.build`` or ``build_library()``.
+Every call recompiles; objects go to ``_build/`` beside this file and the
+library to ``libgsa_hip.so`` in this package directory.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(PKG_DIR, "csrc")
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
+LIB_PATH = os.path.join(PKG_DIR, "libgsa_hip.so")
+ARCH = "gfx950"
+
+HIP_SOURCES = ("indexer.hip", "topk_select.hip", "sparse_attn.hip")
+CXX_SOURCES = ("abi.cpp",)
+
+# Packed fp32 VALU forms are disabled in device code: the compiler would
+# otherwise form v_pk_{add,mul,fma}_f32 from ordinary float code.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+COMMON_FLAGS = ["-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-function"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass reports the device-only feature flag as unknown: drop that line
+    err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+
+
+def build_library(verbose: bool = False, jobs: int = 4) -> str:
+    """Compile every source for gfx950 and link libgsa_hip.so; returns its path."""
+    cc = hipcc()
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    jobs_list = []
+    objs = []
+    for src in HIP_SOURCES + CXX_SOURCES:
+        obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+        cmd = [cc, f"--offload-arch={ARCH}", *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        if src.endswith(".hip"):
+            cmd[2:2] = DEVICE_FLAGS
+        else:
+            cmd = [cc, *COMMON_FLAGS, "-x", "c++", "-c", os.path.join(CSRC, src), "-o", obj]
+        jobs_list.append(cmd)
+        objs.append(obj)
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), jobs_list))
+    tmp = LIB_PATH + ".tmp"
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose="-v" in sys.argv))

@@ -1,0 +1,409 @@
+"""Gated Sparse Attention forward on MI355X: the drop-in module.
+
+Same constructor, forward, ``fuse_projections`` and state_dict keys as the
+reference's ``gsa_triton/gsa_opt.py`` (and ``gsa_ref.py``), so a caller can
+``load_state_dict(ref_state, strict=True)`` and swap the module.  The GEMMs
+stay on PyTorch-ROCm (hipBLASLt); everything else runs in the hand-written
+gfx950 kernels of ``libgsa_hip.so`` through ``_abi``:
+
+  fused projection GEMM -> [indexer stream] gsa_indexer_select (MFMA indexer +
+  exact streaming top-k) || [current stream] gsa_prologue (RoPE k, G2 gate)
+  -> join -> gsa_sparse_attn (RoPE q, gather attention, G1 gate) -> o_proj GEMM
+
+Forward only (inference); there is no autograd support, like the reference's
+Triton kernels.  There is no CPU or eager fallback: the kernels need a GPU and
+the built library, and raise otherwise.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _abi
+
+try:  # roctx ranges on ROCm builds of torch; no-ops elsewhere
+    from torch.cuda import nvtx as _nvtx
+    _range_push, _range_pop = _nvtx.range_push, _nvtx.range_pop
+except Exception:  # pragma: no cover
+    def _range_push(msg: str):
+        pass
+
+    def _range_pop():
+        pass
+
+
+# Width of the fused projection output is padded to a multiple of this many
+# elements so every row (and every slice offset) stays 16-byte aligned.
+FUSED_ALIGN = 64
+
+
+# ---------------------------------------------------------------------------
+# Launchers (gsa_opt.py:143-176, :349-383)
+# ---------------------------------------------------------------------------
+
+def fused_gated_indexer(q_idx: torch.Tensor, k_idx: torch.Tensor, w: torch.Tensor,
+                        bias: torch.Tensor, scale: float, causal: bool = True) -> torch.Tensor:
+    """Indexer scores fp32 [B,T,T] (-inf above the diagonal when causal).
+
+    Same signature as gsa_opt.fused_gated_indexer (gsa_opt.py:143-150); strided
+    views are read in place (no ``.contiguous()`` copies).
+    """
+    _range_push("gsa_hip/indexer_scores")
+    try:
+        return _abi.indexer_scores(q_idx, k_idx, w, bias.detach().float().contiguous(), scale, causal)
+    finally:
+        _range_pop()
+
+
+def fused_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           indices: torch.Tensor, mask: torch.Tensor, scale: float) -> torch.Tensor:
+    """Sparse attention over selected keys (gsa_opt.py:349-356 signature).
+
+    q,k,v [B,T,H,d]; indices [B,T,K] (any integer dtype, any order; clamped
+    to [0, T_kv-1]); mask [B,T,K] bool (True = valid).  Returns q's dtype.
+    """
+    _range_push("gsa_hip/sparse_attn")
+    try:
+        idx = indices.to(torch.int32).contiguous()
+        m = mask.to(torch.uint8).contiguous()
+        q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+        return _abi.sparse_attn(q, k, v, idx, scale, mask=m)
+    finally:
+        _range_pop()
+
+
+# ---------------------------------------------------------------------------
+# RoPE (gsa_opt.py:390-429)
+# ---------------------------------------------------------------------------
+
+def _rope_table(t: torch.Tensor, d: int) -> torch.Tensor:
+    """[T, d] view of a cos/sin table given as [T,d] or broadcastable [1,T,1,d]."""
+    t2 = t.reshape(-1, t.shape[-1])
+    if t2.shape[-1] != d:
+        raise ValueError(f"cos/sin last dim {t2.shape[-1]} != head dim {d}")
+    return t2 if t2.stride(-1) == 1 else t2.contiguous()
+
+
+def apply_rotary_pos_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
+                         sin: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(q*cos + rotate_half(q)*sin, same for k), rounded per op in the input dtype."""
+    d = q.shape[-1]
+    c, s = _rope_table(cos, d), _rope_table(sin, d)
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    q_out, _ = _abi.prologue(k=q, cos=c.to(q.dtype), sin=s.to(q.dtype))
+    k_out, _ = _abi.prologue(k=k, cos=c.to(k.dtype), sin=s.to(k.dtype))
+    return q_out, k_out
+
+
+class RotaryEmbedding(nn.Module):
+    """cos/sin tables with the reference's cache semantics (gsa_opt.py:404-429).
+
+    The cache covers ``max_seq_len`` positions from the fp32 inv_freq at
+    construction and is cast with the module.  A longer request rebuilds it
+    from ``arange(seq_len)`` times the module's current inv_freq (bf16 when
+    the module was cast); the rebuild runs on the host, where the reference's
+    arithmetic runs, and the result moves to the requested device.
+    """
+
+    def __init__(self, dim: int, max_seq_len: int = 8192, base: float = 10000.0):
+        super().__init__()
+        self.dim = dim
+        inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2).float() / dim))
+        self.register_buffer("inv_freq", inv_freq)
+        self._build_cache(max_seq_len, inv_freq)
+
+    def _build_cache(self, seq_len: int, inv_freq: torch.Tensor) -> None:
+        pos = torch.arange(seq_len, dtype=torch.float32)
+        ang = torch.outer(pos, inv_freq.detach().cpu())
+        ang = torch.cat((ang, ang), dim=-1)
+        dev = self.inv_freq.device
+        self.register_buffer("cos_cached", ang.cos().to(dev), persistent=False)
+        self.register_buffer("sin_cached", ang.sin().to(dev), persistent=False)
+
+    def forward(self, seq_len: int, device: torch.device,
+                dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        if seq_len > self.cos_cached.shape[0]:
+            self._build_cache(seq_len, self.inv_freq)
+        cos = self.cos_cached[:seq_len].to(device)
+        sin = self.sin_cached[:seq_len].to(device)
+        if dtype is not None:
+            cos, sin = cos.to(dtype), sin.to(dtype)
+        return cos, sin
+
+
+# ---------------------------------------------------------------------------
+# Sub-modules with the reference's state_dict keys (gsa_opt.py:432-507)
+# ---------------------------------------------------------------------------
+
+class GatedLightningIndexer(nn.Module):
+    """score[q,k] = sum_h sigmoid(w[q,h]) * sigmoid(q_I[q,h].k_I[k]*scale + b[h])."""
+
+    def __init__(self, hidden_size: int, d_indexer: int = 64, n_idx_heads: int = 4):
+        super().__init__()
+        self.d_indexer = d_indexer
+        self.n_idx_heads = n_idx_heads
+        self.scale = 1.0 / math.sqrt(d_indexer)
+        self.idx_q_proj = nn.Linear(hidden_size, n_idx_heads * d_indexer, bias=False)
+        self.idx_k_proj = nn.Linear(hidden_size, d_indexer, bias=False)
+        self.idx_w_proj = nn.Linear(hidden_size, n_idx_heads, bias=True)
+        self.idx_bias = nn.Parameter(torch.zeros(n_idx_heads))
+        nn.init.xavier_uniform_(self.idx_q_proj.weight, gain=1.0)
+        nn.init.xavier_uniform_(self.idx_k_proj.weight, gain=1.0)
+        nn.init.xavier_uniform_(self.idx_w_proj.weight, gain=0.1)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        B, T, _ = x.shape
+        q_idx = self.idx_q_proj(x).view(B, T, self.n_idx_heads, self.d_indexer)
+        k_idx = self.idx_k_proj(x)
+        w = self.idx_w_proj(x)
+        return fused_gated_indexer(q_idx, k_idx, w, self.idx_bias, self.scale, causal=True)
+
+
+class AdaptiveTopKSelector(nn.Module):
+    """Fixed k_eff = min(k_base, k_max, T_kv); k_min is kept but unused, as in
+    the reference (gsa_opt.py:466-483)."""
+
+    def __init__(self, k_base: int = 2048, k_min: int = 256, k_max: int = 4096):
+        super().__init__()
+        self.k_base = k_base
+        self.k_min = k_min
+        self.k_max = k_max
+
+    def k_effective(self, t_kv: int) -> int:
+        return min(self.k_base, self.k_max, t_kv)
+
+    def forward(self, scores: torch.Tensor):
+        """(indices int64 [B,T,k] by (score desc, index asc), mask bool, k_eff)."""
+        B, T, T_kv = scores.shape
+        k_eff = self.k_effective(T_kv)
+        s = scores if scores.dtype == torch.float32 and scores.stride(-1) == 1 else \
+            scores.float().contiguous()
+        _range_push("gsa_hip/topk_select")
+        try:
+            if k_eff <= _abi.TOPK_DESC_MAX_K:
+                idx, _, mask = _abi.topk_select(s, k_eff, _abi.ORDER_SCORE_DESC, want_mask=True)
+                return idx.long(), mask.bool(), k_eff
+            # larger k: exact selection in index order, then a stable device sort by score
+            idx, _, mask = _abi.topk_select(s, k_eff, _abi.ORDER_INDEX_ASC, want_mask=True)
+            idx = idx.long()
+            vals = torch.gather(s, -1, idx).masked_fill(~mask.bool(), -1e9)
+            order = torch.sort(vals, dim=-1, descending=True, stable=True).indices
+            idx = torch.gather(idx, -1, order)
+            return idx, torch.gather(mask.bool(), -1, order), k_eff
+        finally:
+            _range_pop()
+
+    def select_ascending(self, scores: torch.Tensor):
+        """(idx int32 [B,T,k] valid-ascending, count int32 [B,T], k_eff)."""
+        k_eff = self.k_effective(scores.shape[-1])
+        idx, cnt, _ = _abi.topk_select(scores, k_eff, _abi.ORDER_INDEX_ASC)
+        return idx, cnt, k_eff
+
+
+def _gate(v: torch.Tensor, logits: torch.Tensor) -> torch.Tensor:
+    """v * sigmoid(logits), both [B,T,H,d], rounded per op in v's dtype."""
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    _, out = _abi.prologue(v=v, vg=logits)
+    return out
+
+
+class ValueGate(nn.Module):
+    """G2: v = v * sigmoid(W x + b), bias initialised to 0.5."""
+
+    def __init__(self, hidden_size: int):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden_size, hidden_size, bias=True)
+        nn.init.constant_(self.gate_proj.bias, 0.5)
+
+    def forward(self, v: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        B, T, H, d = v.shape
+        return _gate(v, self.gate_proj(x).view(B, T, H, d))
+
+
+class OutputGate(nn.Module):
+    """G1: o = o * sigmoid(W x + b), bias initialised to 0.5."""
+
+    def __init__(self, hidden_size: int):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden_size, hidden_size, bias=True)
+        nn.init.constant_(self.gate_proj.bias, 0.5)
+
+    def forward(self, output: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        B, T, H, d = output.shape
+        return _gate(output, self.gate_proj(x).view(B, T, H, d))
+
+
+# ---------------------------------------------------------------------------
+# The layer (gsa_opt.py:512-730)
+# ---------------------------------------------------------------------------
+
+class GatedSparseAttention(nn.Module):
+    """Drop-in replacement for gsa_ref/gsa_opt.GatedSparseAttention.
+
+    Forward, per layer call:
+      1. one GEMM for the eight projections (weight padded to a multiple of 64
+         output columns; the slices are strided views, never copied);
+      2. indexer stream: gsa_indexer_select -- MFMA indexer fused with the
+         exact top-k, writing ascending int32 indices and per-row counts
+         (the T x T score matrix is never stored);
+         current stream: gsa_prologue -- RoPE(k) and v * sigmoid(vg);
+      3. join, then gsa_sparse_attn -- RoPE(q), gather attention with online
+         softmax, output gate -- and the o_proj GEMM.
+    """
+
+    def __init__(self, hidden_size: int, num_heads: int, k_max: int = 4096, d_indexer: int = 64,
+                 n_idx_heads: int = 4, k_base: int = 2048, k_min: int = 256):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.num_heads = num_heads
+        self.d_head = hidden_size // num_heads
+        self.scale = self.d_head ** -0.5
+
+        self.q_proj = nn.Linear(hidden_size, hidden_size, bias=False)
+        self.k_proj = nn.Linear(hidden_size, hidden_size, bias=False)
+        self.v_proj = nn.Linear(hidden_size, hidden_size, bias=False)
+        self.o_proj = nn.Linear(hidden_size, hidden_size, bias=False)
+
+        self.indexer = GatedLightningIndexer(hidden_size, d_indexer, n_idx_heads)
+        self.topk_selector = AdaptiveTopKSelector(k_base, k_min, k_max)
+        self.value_gate = ValueGate(hidden_size)
+        self.output_gate = OutputGate(hidden_size)
+        self.rotary_emb = RotaryEmbedding(self.d_head)
+
+        self._fused_weight: Optional[torch.Tensor] = None
+        self._fused_bias: Optional[torch.Tensor] = None
+        self._proj_sizes = [
+            hidden_size, hidden_size, hidden_size, hidden_size, hidden_size,
+            n_idx_heads * d_indexer, d_indexer, n_idx_heads,
+        ]
+        total = sum(self._proj_sizes)
+        self._fused_width = (total + FUSED_ALIGN - 1) // FUSED_ALIGN * FUSED_ALIGN
+        self._indexer_stream: Optional[torch.cuda.Stream] = None
+        # Optional per-kernel timing hook: a list to which forward appends
+        # (start, end) event pairs around the sparse-attention launch.
+        self.attn_events: Optional[list] = None
+        self.register_load_state_dict_post_hook(lambda mod, _keys: mod._drop_fused())
+
+    # -- fused projection weight -------------------------------------------
+    def _drop_fused(self) -> None:
+        self._fused_weight = None
+        self._fused_bias = None
+
+    def fuse_projections(self) -> None:
+        """Build the fused, padded projection weight/bias.  Call after load_state_dict()."""
+        w = torch.cat([
+            self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
+            self.value_gate.gate_proj.weight, self.output_gate.gate_proj.weight,
+            self.indexer.idx_q_proj.weight, self.indexer.idx_k_proj.weight,
+            self.indexer.idx_w_proj.weight,
+        ], dim=0).detach()
+        pad = self._fused_width - w.shape[0]
+        if pad:
+            w = torch.cat([w, w.new_zeros(pad, w.shape[1])], dim=0)
+        bias = w.new_zeros(self._fused_width)
+        off = self._offsets()
+        D = self.hidden_size
+        bias[off["vg"]:off["vg"] + D] = self.value_gate.gate_proj.bias.detach()
+        bias[off["og"]:off["og"] + D] = self.output_gate.gate_proj.bias.detach()
+        bias[off["iw"]:off["iw"] + self.indexer.n_idx_heads] = self.indexer.idx_w_proj.bias.detach()
+        self._fused_weight = w.contiguous()
+        self._fused_bias = bias
+
+    def _get_fused_weight(self, like: Optional[torch.Tensor] = None):
+        fw = self._fused_weight
+        if fw is None or (like is not None and (fw.device != like.device or fw.dtype != like.dtype)):
+            self.fuse_projections()
+        return self._fused_weight, self._fused_bias
+
+    def _offsets(self):
+        names = ("q", "k", "v", "vg", "og", "iq", "ik", "iw")
+        off, acc = {}, 0
+        for n, sz in zip(names, self._proj_sizes):
+            off[n] = acc
+            acc += sz
+        return off
+
+    # -- forward pieces (also used by tests) -------------------------------
+    def project(self, x: torch.Tensor):
+        """Fused GEMM; returns a dict of strided [B,T,...] views into one buffer."""
+        B, T, D = x.shape
+        H, d = self.num_heads, self.d_head
+        Hi, di = self.indexer.n_idx_heads, self.indexer.d_indexer
+        w, b = self._get_fused_weight(x)
+        comb = F.linear(x, w, b)
+        off = self._offsets()
+        v = {}
+        for n in ("q", "k", "v", "vg", "og"):
+            v[n] = comb[..., off[n]:off[n] + D].view(B, T, H, d)
+        v["iq"] = comb[..., off["iq"]:off["iq"] + Hi * di].view(B, T, Hi, di)
+        v["ik"] = comb[..., off["ik"]:off["ik"] + di]
+        v["iw"] = comb[..., off["iw"]:off["iw"] + Hi]
+        v["_buf"] = comb
+        return v
+
+    def select(self, views, T: int):
+        """Fused indexer + top-k on the current stream -> (idx int32, count int32)."""
+        k_eff = self.topk_selector.k_effective(T)
+        bias = self.indexer.idx_bias.detach().float().contiguous()
+        return _abi.indexer_select(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale, k_eff)
+
+    def forward(self, x: torch.Tensor, attention_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError("GatedSparseAttention (HIP) needs a device tensor")
+        B, T, D = x.shape
+        if D != self.hidden_size:
+            raise ValueError(f"hidden size {D} != {self.hidden_size}")
+        _range_push("gsa_hip/forward")
+        dev = x.device
+        cur = torch.cuda.current_stream(dev)
+
+        _range_push("gsa_hip/fused_gemm")
+        views = self.project(x)
+        _range_pop()
+
+        # Track A: indexer + top-k on the side stream
+        if self._indexer_stream is None or self._indexer_stream.device != dev:
+            self._indexer_stream = torch.cuda.Stream(device=dev)
+        side = self._indexer_stream
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            _range_push("gsa_hip/indexer_select")
+            idx, cnt = self.select(views, T)
+            _range_pop()
+
+        # Track B: RoPE(k) and the value gate on the current stream
+        _range_push("gsa_hip/prologue")
+        cos, sin = self.rotary_emb(T, dev, x.dtype)
+        cos, sin = cos.contiguous(), sin.contiguous()
+        k_rope, v_gated = _abi.prologue(k=views["k"], v=views["v"], vg=views["vg"], cos=cos, sin=sin)
+        _range_pop()
+
+        cur.wait_stream(side)
+        idx.record_stream(cur)
+        cnt.record_stream(cur)
+        views["_buf"].record_stream(side)
+
+        _range_push("gsa_hip/sparse_attn")
+        ev = None
+        if self.attn_events is not None:
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record(cur)
+        attn = _abi.sparse_attn(views["q"], k_rope, v_gated, idx, self.scale, count=cnt,
+                                og=views["og"], cos=cos, sin=sin,
+                                flags=_abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE)
+        if ev is not None:
+            ev[1].record(cur)
+            self.attn_events.append(ev)
+        _range_pop()
+
+        _range_push("gsa_hip/o_proj")
+        out = F.linear(attn.view(B, T, D), self.o_proj.weight)
+        _range_pop()
+        _range_pop()
+        return out

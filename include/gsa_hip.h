@@ -1,0 +1,169 @@
+/*
+ * gsa_hip.h -- C ABI of libgsa_hip.so, the MI355X (gfx950) kernels of the
+ * Gated Sparse Attention (GSA) layer forward.
+ *
+ * Each entry point replaces one step of the reference's optimized forward
+ * (gsa_triton/gsa_opt.py); the reference line it replaces is cited above it.
+ *
+ * Conventions
+ *  - Plain pointers and sizes; no framework types.  Device pointers are HIP
+ *    device pointers; `stream` is a hipStream_t (NULL = the null stream).
+ *  - Tensors are [B, T, ...] with the innermost dimensions (heads, then
+ *    elements) contiguous; each tensor is described by its pointer and its
+ *    batch and row strides, in elements.  Strided views into one fused
+ *    projection output are therefore accepted without copies.
+ *  - dtype is GSA_DTYPE_BF16 or GSA_DTYPE_F32 for every floating tensor of a
+ *    call (indices and counts are int32, masks uint8, scores and bias fp32).
+ *  - Ownership: the caller owns every buffer.  The library never allocates,
+ *    frees or retains device memory and never synchronises; every call is
+ *    enqueued on `stream` and returns.
+ *  - Errors: 0 on success; > 0 for argument errors, detected on the host
+ *    before anything is enqueued; < 0 is the negated hipError_t of a failed
+ *    launch.  gsa_status_string() names every code.
+ *  - Thread safety: all entry points are reentrant.
+ */
+#ifndef GSA_HIP_H
+#define GSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GSA_ABI_VERSION 1
+
+#define GSA_DTYPE_F32  0
+#define GSA_DTYPE_BF16 1
+
+#define GSA_OK            0
+#define GSA_ERR_NULL      1  /* a required pointer is NULL                        */
+#define GSA_ERR_SHAPE     2  /* unsupported or inconsistent sizes                 */
+#define GSA_ERR_DTYPE     3  /* unknown dtype code                                */
+#define GSA_ERR_ALIGN     4  /* pointer or stride breaks the vector-load alignment */
+#define GSA_ERR_K         5  /* k out of range (k < 1, k > keys, or too large)     */
+#define GSA_ERR_FLAGS     6  /* unknown flag or order code                         */
+
+/* Order of gsa_topk_select's output */
+#define GSA_ORDER_INDEX_ASC  0  /* valid indices ascending, then invalid ones ascending */
+#define GSA_ORDER_SCORE_DESC 1  /* by (score desc, index asc): torch.topk's sorted order */
+
+/* Flags of gsa_sparse_attn */
+#define GSA_ATTN_ROPE_Q   1  /* q is pre-RoPE: apply RoPE with cos/sin in the prologue  */
+#define GSA_ATTN_OUT_GATE 2  /* multiply the output by sigmoid(og) (the G1 output gate) */
+
+/* Largest k_eff of gsa_topk_select in GSA_ORDER_SCORE_DESC order. */
+#define GSA_TOPK_DESC_MAX_K 4096
+
+int gsa_abi_version(void);
+const char* gsa_status_string(int status);
+
+/*
+ * Fused gated lightning indexer, full score matrix.
+ * Replaces fused_gated_indexer (gsa_triton/gsa_opt.py:143-176) and its kernel
+ * (gsa_opt.py:38-140); semantics of GatedLightningIndexer.forward
+ * (gsa_triton/gsa_ref.py:97-126):
+ *   scores[b,i,j] = sum_h sigmoid(w[b,i,h]) * sigmoid(scale*<q[b,i,h,:], k[b,j,:]> + bias[h])
+ *   for j <= i (or every j when causal == 0), -inf otherwise.
+ * q_idx [B,T,Hi,di], k_idx [B,T,di], w [B,T,Hi] in dtype; bias fp32 [Hi];
+ * scores fp32 [B,T,T] with strides (s_sb, s_st), unit column stride.
+ * Supported: Hi == 4, di == 64.
+ */
+int gsa_indexer_scores(const void* q_idx, int64_t q_sb, int64_t q_st,
+                       const void* k_idx, int64_t k_sb, int64_t k_st,
+                       const void* w, int64_t w_sb, int64_t w_st,
+                       const float* bias, float scale,
+                       int B, int T, int Hi, int di, int causal, int dtype,
+                       float* scores, int64_t s_sb, int64_t s_st,
+                       void* stream);
+
+/*
+ * Exact per-row top-k of an fp32 score matrix.
+ * Replaces AdaptiveTopKSelector.forward (gsa_triton/gsa_opt.py:473-483,
+ * gsa_triton/gsa_ref.py:138-150) and the ascending re-sort of the optimized
+ * forward (gsa_opt.py:674-677).
+ * Row r of scores [B,T,Tkv] selects the k_eff largest after mapping -inf to
+ * -1e9 (NaN ranks above +inf); ties at the k-th value go to the lowest
+ * indices.  An entry is valid when its score is not -inf.
+ *   order GSA_ORDER_INDEX_ASC : idx_out row = valid selected ascending, then
+ *                               invalid selected ascending; count = #valid.
+ *   order GSA_ORDER_SCORE_DESC: idx_out row sorted by (score desc, index asc);
+ *                               k_eff <= GSA_TOPK_DESC_MAX_K.
+ * idx_out int32 [B,T,k_eff] contiguous; count_out int32 [B,T] (nullable);
+ * mask_out uint8 [B,T,k_eff] (nullable): 1 where the entry is valid.
+ */
+int gsa_topk_select(const float* scores, int64_t s_sb, int64_t s_st,
+                    int B, int T, int Tkv, int k_eff, int order,
+                    int32_t* idx_out, int32_t* count_out, uint8_t* mask_out,
+                    void* stream);
+
+/*
+ * Indexer and selector fused: the [B,T,T] score matrix is never stored.
+ * Replaces the indexer track of the optimized forward (gsa_triton/gsa_opt.py:
+ * 663-677: fused_gated_indexer + AdaptiveTopKSelector + ascending sort).
+ * Produces exactly what gsa_indexer_scores followed by gsa_topk_select
+ * (GSA_ORDER_INDEX_ASC, causal) produce: idx_out int32 [B,T,k_eff] holds row
+ * t's min(t+1, k_eff) selected keys ascending, followed by t+1, t+2, ... for
+ * rows with fewer than k_eff causal keys; count_out int32 [B,T].
+ * Supported: Hi == 4, di == 64, 1 <= k_eff <= T.
+ */
+int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
+                       const void* k_idx, int64_t k_sb, int64_t k_st,
+                       const void* w, int64_t w_sb, int64_t w_st,
+                       const float* bias, float scale,
+                       int B, int T, int Hi, int di, int k_eff, int dtype,
+                       int32_t* idx_out, int32_t* count_out,
+                       void* stream);
+
+/*
+ * Producer pass over the projection output: RoPE on k and the G2 value gate.
+ * Replaces gsa_triton/gsa_opt.py:685-697 (v * sigmoid(vg), RoPE on k).
+ *   k_out = k*cos + rotate_half(k)*sin,  v_out = v * sigmoid(vg)
+ * with each op rounded in dtype as the reference rounds it.  Either half may
+ * be skipped: k == NULL skips RoPE (cos, sin, k_out unused), v == NULL skips
+ * the gate (vg, v_out unused); the same halves back apply_rotary_pos_emb
+ * (gsa_opt.py:396-401) and ValueGate/OutputGate (gsa_opt.py:486-507).
+ * k, v, vg [B,T,H,d]; cos, sin [T,d] (row stride cs_st) in dtype;
+ * k_out, v_out contiguous [B,T,H,d].  Supported: d == 128, 1 <= H <= 64.
+ */
+int gsa_prologue(const void* k, int64_t k_sb, int64_t k_st,
+                 const void* v, int64_t v_sb, int64_t v_st,
+                 const void* vg, int64_t g_sb, int64_t g_st,
+                 const void* cos, const void* sin, int64_t cs_st,
+                 int B, int T, int H, int d, int dtype,
+                 void* k_out, void* v_out,
+                 void* stream);
+
+/*
+ * Sparse attention over per-row selected keys (gather, online softmax).
+ * Replaces fused_sparse_attention (gsa_triton/gsa_opt.py:349-383) and its
+ * kernel (gsa_opt.py:187-346); with GSA_ATTN_ROPE_Q it also applies RoPE to q
+ * (gsa_opt.py:692-697) and with GSA_ATTN_OUT_GATE the G1 gate
+ * (gsa_opt.py:699-701, 719-721).  Semantics of sparse_attention_ref
+ * (gsa_triton/gsa_ref.py:202-238): for every (b,t,h),
+ *   out = sum_m softmax_m(scale * <q, k[idx_m]>) v[idx_m]
+ * over the valid entries m (all masked -> 0).  Entry m of row (b,t) is valid
+ * when m < count[b,t] (count may be NULL: all k_sel entries) and
+ * mask[b,t,m] != 0 (mask may be NULL).  Indices are clamped to [0, Tkv-1].
+ * q [B,T,H,d], k, v [B,Tkv,H,d], og [B,T,H,d], out [B,T,H,d] in dtype;
+ * idx int32 and mask uint8 share the strides (i_sb, i_st); count int32 [B,T].
+ * Supported: d == 128, 1 <= H <= 64.
+ */
+int gsa_sparse_attn(const void* q, int64_t q_sb, int64_t q_st,
+                    const void* k, int64_t k_sb, int64_t k_st,
+                    const void* v, int64_t v_sb, int64_t v_st,
+                    const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel,
+                    const int32_t* count, const uint8_t* mask,
+                    const void* og, int64_t o_sb, int64_t o_st,
+                    const void* cos, const void* sin, int64_t cs_st,
+                    void* out, int64_t out_sb, int64_t out_st,
+                    int B, int T, int Tkv, int H, int d, float scale,
+                    int dtype, int flags,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSA_HIP_H */

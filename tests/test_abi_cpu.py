@@ -1,0 +1,150 @@
+"""The C ABI library without a GPU: it loads, exports every declared symbol,
+and rejects bad arguments on the host before anything is enqueued."""
+
+import os
+import re
+
+import pytest
+
+from gsa_gdn_benchmarkstudy_amd import _abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gsa_hip.h")
+
+# Fake device addresses: never dereferenced, every call below is rejected
+# before a launch.
+P = 0x10000          # 16-byte aligned
+MIS = 0x10002        # 2-byte aligned only
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gsa_\w+)\s*\(", text)))
+
+
+def _macros():
+    text = open(HEADER).read()
+    return {k: int(v) for k, v in re.findall(r"#define\s+(GSA_\w+)\s+(-?\d+)\b", text)}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _abi.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    decl = _declared()
+    assert decl == sorted(_abi.EXPORTS)
+    for name in decl:
+        assert hasattr(lib, name), name
+
+
+def test_constants_match_header(lib):
+    m = _macros()
+    assert lib.gsa_abi_version() == m["GSA_ABI_VERSION"] == _abi.ABI_VERSION
+    assert (m["GSA_DTYPE_F32"], m["GSA_DTYPE_BF16"]) == (_abi.DTYPE_F32, _abi.DTYPE_BF16)
+    assert (m["GSA_ORDER_INDEX_ASC"], m["GSA_ORDER_SCORE_DESC"]) == (_abi.ORDER_INDEX_ASC, _abi.ORDER_SCORE_DESC)
+    assert (m["GSA_ATTN_ROPE_Q"], m["GSA_ATTN_OUT_GATE"]) == (_abi.ATTN_ROPE_Q, _abi.ATTN_OUT_GATE)
+    assert m["GSA_TOPK_DESC_MAX_K"] == _abi.TOPK_DESC_MAX_K
+
+
+def test_status_strings(lib):
+    for code in range(0, 7):
+        assert _abi.status_string(code) not in ("", "unknown status")
+    assert "HIP" in _abi.status_string(-1)
+    assert _abi.status_string(99) == "unknown status"
+
+
+def _scores(lib, **kw):
+    a = dict(q=P, qsb=0, qst=256, k=P, ksb=0, kst=64, w=P, wsb=0, wst=4, bias=P, scale=0.125,
+             B=1, T=32, Hi=4, di=64, causal=1, dtype=1, out=P, osb=0, ost=32)
+    a.update(kw)
+    return lib.gsa_indexer_scores(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["w"], a["wsb"],
+                                  a["wst"], a["bias"], a["scale"], a["B"], a["T"], a["Hi"], a["di"],
+                                  a["causal"], a["dtype"], a["out"], a["osb"], a["ost"], None)
+
+
+def test_indexer_scores_validation(lib):
+    assert _scores(lib, q=None) == 1
+    assert _scores(lib, out=None) == 1
+    assert _scores(lib, dtype=7) == 3
+    assert _scores(lib, Hi=8) == 2
+    assert _scores(lib, di=32) == 2
+    assert _scores(lib, T=0) == 2
+    assert _scores(lib, q=MIS) == 4
+    assert _scores(lib, qst=260) == 4        # row stride not a multiple of 8 bf16
+
+
+def _select(lib, **kw):
+    a = dict(q=P, qsb=0, qst=256, k=P, ksb=0, kst=64, w=P, wsb=0, wst=4, bias=P, scale=0.125,
+             B=1, T=32, Hi=4, di=64, k_eff=8, dtype=1, idx=P, cnt=P)
+    a.update(kw)
+    return lib.gsa_indexer_select(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["w"], a["wsb"],
+                                  a["wst"], a["bias"], a["scale"], a["B"], a["T"], a["Hi"], a["di"],
+                                  a["k_eff"], a["dtype"], a["idx"], a["cnt"], None)
+
+
+def test_indexer_select_validation(lib):
+    assert _select(lib, bias=None) == 1
+    assert _select(lib, cnt=None) == 1
+    assert _select(lib, k_eff=0) == 5
+    assert _select(lib, k_eff=33) == 5
+    assert _select(lib, dtype=-1) == 3
+    assert _select(lib, k=MIS) == 4
+
+
+def test_topk_validation(lib):
+    f = lib.gsa_topk_select
+    assert f(None, 0, 32, 1, 32, 32, 4, 0, P, P, None, None) == 1
+    assert f(P, 0, 32, 1, 32, 32, 0, 0, P, P, None, None) == 5
+    assert f(P, 0, 32, 1, 32, 32, 33, 0, P, P, None, None) == 5
+    assert f(P, 0, 8192, 1, 8, 8192, 5000, 1, P, P, None, None) == 5   # desc order k cap
+    assert f(P, 0, 32, 1, 32, 32, 4, 9, P, P, None, None) == 6
+    assert f(P, 0, 32, 0, 32, 32, 4, 0, P, P, None, None) == 2
+    assert f(P + 2, 0, 32, 1, 32, 32, 4, 0, P, P, None, None) == 4
+
+
+def test_prologue_validation(lib):
+    f = lib.gsa_prologue
+    ok = dict(k=P, ksb=0, kst=2048, v=P, vsb=0, vst=2048, g=P, gsb=0, gst=2048, cos=P, sin=P, cst=128,
+              B=1, T=4, H=16, d=128, dtype=1, ko=P, vo=P)
+
+    def call(**kw):
+        a = dict(ok)
+        a.update(kw)
+        return f(a["k"], a["ksb"], a["kst"], a["v"], a["vsb"], a["vst"], a["g"], a["gsb"], a["gst"],
+                 a["cos"], a["sin"], a["cst"], a["B"], a["T"], a["H"], a["d"], a["dtype"], a["ko"], a["vo"], None)
+
+    assert call(k=None, v=None) == 1
+    assert call(cos=None) == 1
+    assert call(g=None) == 1
+    assert call(d=64) == 2
+    assert call(H=65) == 2
+    assert call(dtype=5) == 3
+    assert call(vo=MIS) == 4
+    assert call(kst=2052) == 4
+
+
+def test_sparse_attn_validation(lib):
+    f = lib.gsa_sparse_attn
+    ok = dict(q=P, qsb=0, qst=2048, k=P, ksb=0, kst=2048, v=P, vsb=0, vst=2048, idx=P, isb=0, ist=8, ksel=8,
+              cnt=P, mask=None, og=P, osb=0, ost=2048, cos=P, sin=P, cst=128, out=P, outsb=0, outst=2048,
+              B=1, T=4, Tkv=4, H=16, d=128, scale=0.088, dtype=1, flags=3)
+
+    def call(**kw):
+        a = dict(ok)
+        a.update(kw)
+        return f(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["v"], a["vsb"], a["vst"],
+                 a["idx"], a["isb"], a["ist"], a["ksel"], a["cnt"], a["mask"], a["og"], a["osb"], a["ost"],
+                 a["cos"], a["sin"], a["cst"], a["out"], a["outsb"], a["outst"], a["B"], a["T"], a["Tkv"],
+                 a["H"], a["d"], a["scale"], a["dtype"], a["flags"], None)
+
+    assert call(idx=None) == 1
+    assert call(og=None) == 1                 # OUT_GATE without og
+    assert call(cos=None) == 1                # ROPE_Q without tables
+    assert call(flags=8) == 6
+    assert call(d=96) == 2
+    assert call(ksel=-1) == 5
+    assert call(q=MIS) == 4
+    assert call(idx=P + 2) == 4
