@@ -93,12 +93,13 @@ template <typename T> struct KV;
 template <> struct KV<uint16_t> {
   u32x4 r;
   __device__ void load(const uint16_t* p) { r = *reinterpret_cast<const u32x4*>(p); }
-  __device__ float dot(const u32x4& qp) const {
+  __device__ float dot(const float (&q)[8]) const {
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, qp[i]),
-                                            __builtin_bit_cast(bf16x2, r[i]), acc, false);
+    for (int i = 0; i < 4; ++i) {
+      acc = __builtin_fmaf(q[2 * i], bf16lo(r[i]), acc);
+      acc = __builtin_fmaf(q[2 * i + 1], bf16hi(r[i]), acc);
+    }
     return acc;
   }
   __device__ void axpy(float p, float (&acc)[8]) const {
@@ -131,17 +132,8 @@ template <> struct KV<float> {
   }
 };
 
-// q held in the operand form KV<T>::dot takes.
-template <typename T> struct QReg;
-template <> struct QReg<uint16_t> {
-  u32x4 r;
-  __device__ void set(const float (&x)[8]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = pack_bf16(x[2 * i], x[2 * i + 1]);
-  }
-  __device__ const u32x4& op() const { return r; }
-};
-template <> struct QReg<float> {
+// q held as fp32 (exact for bf16 inputs).
+struct QReg {
   float r[8];
   __device__ void set(const float (&x)[8]) {
 #pragma unroll
@@ -171,7 +163,7 @@ __global__ __launch_bounds__(kThreads) void sparse_attn_kernel(AttnArgs p) {
     load8(static_cast<const T*>(p.sin) + (int64_t)t * p.cs_st + li * 8, s);
     rope8<T>(xq, c, s, li);
   }
-  QReg<T> q;
+  QReg q;
   q.set(xq);
 
   const int32_t* irow = p.idx + b * p.i_sb + (int64_t)t * p.i_st;

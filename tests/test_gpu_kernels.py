@@ -130,7 +130,7 @@ def test_indexer_select_all_ties_overflow_path(dev, T, k):
     """q = 0: every score of a row is equal, so one bin holds the whole row and the
     radix-digit passes resolve it; the lowest indices win."""
     _log(f"indexer_select all-ties T={T} k={k}")
-    buf, q, k_, w, bias = _indexer_inputs(1, T, torch.bfloat16, seed=5)
+    buf, q, k_, w, bias = _indexer_inputs(1, T, torch.bfloat16, seed=5, pad=4)
     buf[..., :256] = 0
     bd = buf.to(dev)
     qd = bd[..., :256].view(1, T, 4, 64)
@@ -148,8 +148,8 @@ def test_indexer_select_overlap_c2(dev):
     _log("indexer_select overlap c2 T=4096")
     g = torch.Generator().manual_seed(0)
     x = torch.randn(1, T, 2048, generator=g).to(torch.bfloat16)
-    W = (torch.randn(324, 2048, generator=g) * 0.02).to(torch.bfloat16)
-    proj = torch.nn.functional.linear(x.to(dev), W.to(dev))          # [1,T,324] bf16 on the GPU
+    W = (torch.randn(328, 2048, generator=g) * 0.02).to(torch.bfloat16)   # rows padded to 16 bytes
+    proj = torch.nn.functional.linear(x.to(dev), W.to(dev))          # [1,T,328] bf16 on the GPU
     q, kk, w = proj[..., :256].view(1, T, 4, 64), proj[..., 256:320], proj[..., 320:324]
     bias = torch.zeros(4)
     fi, fc = _abi.indexer_select(q, kk, w, bias.to(dev), 0.125, k)
@@ -240,8 +240,14 @@ def test_sparse_attention_fused_rope_gate_count(dev, dtype):
     mask = torch.arange(k)[None, None, :] < cnt[..., None]
     att = orc.sparse_attention(qr.double(), kk.double(), v.double(), ia, mask, 128 ** -0.5)
     if dtype == torch.bfloat16:
+        # two bf16 roundings in a row (attention cast, gated product), each within
+        # one ulp (<= 2^-7 relative) of the reference's: <= 2 ulps everywhere,
+        # <= 1 ulp on all but 1% of the elements
         ref = (att.to(dtype) * torch.sigmoid(og)).double()
-        assert torch.all((out.double() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-6)
+        diff = (out.double() - ref).abs()
+        _log(f"  max rel {(diff / (ref.abs() + 1e-6)).max().item():.3e}")
+        assert torch.all(diff <= ref.abs() * 2 ** -6 + 1e-6)
+        assert (diff > ref.abs() * 2 ** -7 + 1e-6).double().mean() < 0.01
     else:
         ref = att * torch.sigmoid(og.double())
         assert torch.allclose(out.double(), ref, atol=1e-5, rtol=1e-5)
