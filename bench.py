@@ -64,6 +64,20 @@ def indexer_flops(B, T):
     return 2 * B * HI * DI * T * (T + 1) // 2
 
 
+def profiled_traffic(kernel, config):
+    """HBM-side bytes per launch of `kernel` at `config`, from the committed rocprofv3
+    PMC summary (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration), or None."""
+    path = os.path.join(ROOT, "profiles", f"sparse_attn_{config}_pmc.md")
+    try:
+        for line in open(path):
+            f = line.split()
+            if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == kernel and f[2] == config:
+                return int(f[3])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(B, T, budget_s, dtype=torch.bfloat16):
     """The CPU oracle (restatement of gsa_ref.py's forward) on sampled query rows
     of the same workload: per-token cost = the token's own projections plus its
@@ -120,6 +134,8 @@ def main():
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c3")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after timing, run one plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -172,6 +188,15 @@ def main():
         idx_ms = e0.elapsed_time(e1) / n_idx
         del views
 
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     abytes, P = attn_bytes(B, T, k_eff)
     achieved = abytes / (attn_ms * 1e-3) / 1e9
     fidx = indexer_flops(B, T)
@@ -195,7 +220,8 @@ def main():
                                f"k_eff={k_eff} causal", "name": args.config, "batch": B, "seq_len": T,
                    "k_eff": k_eff},
         "roofline": {"kernel": "gsa_sparse_attn", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": profiled_traffic("gsa_sparse_attn", args.config),
                      "algorithmic_bytes": abytes, "valid_pairs": P, "ms": attn_ms},
         "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,
                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": idx_tflops / BF16_PEAK_TFLOPS,
