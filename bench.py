@@ -5,7 +5,9 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--cpu-seconds
 
 One step = one GatedSparseAttention forward over one batch of synthetic input
 already resident in HBM (fused projection GEMM, fused indexer + exact top-k,
-RoPE/gate producer, sparse gather-attention with the output gate, o_proj).
+RoPE/gate producer, sparse attention with the output gate, o_proj), with the
+module's default attention kernel (block-dense MFMA for bf16).  The gather
+attention kernel is timed on the same layer and input for its HBM roofline.
 Prints ONE JSON line.
 """
 
@@ -66,15 +68,17 @@ def indexer_flops(B, T):
 
 def profiled_traffic(kernel, config):
     """HBM-side bytes per launch of `kernel` at `config`, from the committed rocprofv3
-    PMC summary (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration), or None."""
-    path = os.path.join(ROOT, "profiles", f"sparse_attn_{config}_pmc.md")
+    PMC summaries (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration), or None."""
+    pdir = os.path.join(ROOT, "profiles")
     try:
-        for line in open(path):
+        names = sorted(f for f in os.listdir(pdir) if f.endswith("_pmc.md"))
+    except OSError:
+        return None
+    for name in names:
+        for line in open(os.path.join(pdir, name)):
             f = line.split()
             if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == kernel and f[2] == config:
                 return int(f[3])
-    except OSError:
-        pass
     return None
 
 
@@ -172,7 +176,25 @@ def main():
         model.attn_events = None
     total_ms = start.elapsed_time(end)
     ms = total_ms / args.steps
+    attn_impl = "dense" if model.uses_dense(dtype) else "gather"
     attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+
+    # the gather kernel on the same layer and input, timed the same way
+    gather_ms = None
+    if attn_impl == "dense":
+        with torch.no_grad():
+            model.attn_impl = "gather"
+            model(x)
+            torch.cuda.synchronize()
+            model.attn_events = []
+            for _ in range(min(args.steps, 5)):
+                model(x)
+            torch.cuda.synchronize()
+            gather_ms = sum(a.elapsed_time(b) for a, b in model.attn_events) / len(model.attn_events)
+            model.attn_events = None
+            model.attn_impl = "auto"
+    else:
+        gather_ms = attn_ms
 
     # indexer kernel alone (same stream discipline, timed separately)
     with torch.no_grad():
@@ -198,9 +220,25 @@ def main():
         del src, dst
 
     abytes, P = attn_bytes(B, T, k_eff)
-    achieved = abytes / (attn_ms * 1e-3) / 1e9
+    gather_gbs = abytes / (gather_ms * 1e-3) / 1e9
+    aflops = 4 * P * H * DH                     # useful (selected-pair) QK and PV flops
     fidx = indexer_flops(B, T)
     idx_tflops = fidx / (idx_ms * 1e-3) / 1e12
+    gather_roof = {"kernel": "gsa_sparse_attn", "bound": "hbm", "achieved": gather_gbs, "peak": HBM_PEAK_GBS,
+                   "unit": "GB/s", "frac": gather_gbs / HBM_PEAK_GBS,
+                   "traffic": profiled_traffic("gsa_sparse_attn", args.config),
+                   "algorithmic_bytes": abytes, "valid_pairs": P, "ms": gather_ms}
+    if attn_impl == "dense":
+        nqb = (T + 63) // 64
+        dense_flops = 4 * B * H * DH * 64 * 64 * sum(min(qb * 64 + 63, T - 1) // 64 + 1 for qb in range(nqb))
+        ach = aflops / (attn_ms * 1e-3) / 1e12
+        roofline = {"kernel": "gsa_dense_attn", "bound": "mfma", "achieved": ach, "peak": BF16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": ach / BF16_PEAK_TFLOPS,
+                    "traffic": profiled_traffic("gsa_dense_attn", args.config),
+                    "algorithmic_flops": aflops, "executed_flops": dense_flops,
+                    "executed_tflops": dense_flops / (attn_ms * 1e-3) / 1e12, "ms": attn_ms}
+    else:
+        roofline = gather_roof
 
     out = {
         "metric": METRIC,
@@ -219,10 +257,8 @@ def main():
         "config": {"workload": f"GSA layer forward B={B} T={T} D={D} H={H} d={DH} H_idx={HI} d_idx={DI} "
                                f"k_eff={k_eff} causal", "name": args.config, "batch": B, "seq_len": T,
                    "k_eff": k_eff},
-        "roofline": {"kernel": "gsa_sparse_attn", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": profiled_traffic("gsa_sparse_attn", args.config),
-                     "algorithmic_bytes": abytes, "valid_pairs": P, "ms": attn_ms},
+        "roofline": roofline,
+        "gather_attention": gather_roof,
         "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,
                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": idx_tflops / BF16_PEAK_TFLOPS,
                     "flops": fidx, "ms": idx_ms},

@@ -32,7 +32,8 @@ ATTN_OUT_GATE = 2
 # Every symbol include/gsa_hip.h declares.
 EXPORTS = (
     "gsa_abi_version", "gsa_status_string", "gsa_indexer_scores", "gsa_topk_select",
-    "gsa_indexer_select", "gsa_prologue", "gsa_sparse_attn",
+    "gsa_indexer_select", "gsa_prologue", "gsa_sparse_attn", "gsa_prologue_vt",
+    "gsa_selection_mask", "gsa_dense_attn",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -50,6 +51,12 @@ _PROTOS = {
     "gsa_sparse_attn": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                          _vp, _i64, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
                          _vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp], _i32),
+    "gsa_prologue_vt": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
+                         _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp], _i32),
+    "gsa_selection_mask": ([_vp, _i64, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp], _i32),
+    "gsa_dense_attn": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i64, _i64,
+                        _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64,
+                        _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp], _i32),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -272,4 +279,103 @@ def sparse_attn(q, k, v, idx, scale: float, count=None, mask=None, og=None, cos=
                              _ptr(out), *_rows(out, HD), B, T, Tkv, H, d, float(scale),
                              dtype_code(q.dtype), int(flags), _stream(q))
     _check(st, "gsa_sparse_attn")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Block-dense attention path
+# ---------------------------------------------------------------------------
+
+def vt_len(T: int) -> int:
+    """Row length of the transposed V buffer: T rounded up to a multiple of 64."""
+    return (T + 63) // 64 * 64
+
+
+def mask_words(Tkv: int) -> int:
+    """uint32 words per row of a selection bitmask."""
+    return 2 * ((Tkv + 63) // 64)
+
+
+def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None):
+    """RoPE(k) -> k_out [B,T,H,d] and (v*sigmoid(vg))^T -> vt [B,H,d,ldv] (bf16)."""
+    lib = load()
+    _need_cuda(k, v, vg, cos, sin)
+    B, T, H, d = v.shape
+    HD = H * d
+    ldv = vt_len(T)
+    for t, nm in ((k, "k"), (vg, "vg"), (k_out, "k_out")):
+        if t is not None:
+            _expect(tuple(t.shape) == (B, T, H, d) and t.dtype == v.dtype, f"{nm}: {v.dtype} [B,T,H,d]")
+    if k is not None:
+        _expect(cos is not None and sin is not None and cos.dim() == 2 and cos.shape[0] >= T
+                and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape) and cos.dtype == sin.dtype == v.dtype
+                and cos.stride(1) == 1 and sin.stride() == cos.stride(), "cos/sin: [>=T, d] in v's dtype")
+        if k_out is None:
+            k_out = torch.empty(B, T, H, d, device=v.device, dtype=v.dtype)
+        _expect(k_out.is_contiguous(), "k_out must be contiguous")
+    if vt is None:
+        vt = torch.empty(B, H, d, ldv, device=v.device, dtype=v.dtype)
+    _expect(tuple(vt.shape) == (B, H, d, ldv) and vt.is_contiguous() and vt.dtype == v.dtype,
+            "vt: contiguous [B,H,d,ldv]")
+    ks = _rows(k, HD) if k is not None else (0, 0)
+    cs = cos.stride(0) if cos is not None else 0
+    st = lib.gsa_prologue_vt(_ptr(k), *ks, _ptr(v), *_rows(v, HD), _ptr(vg), *_rows(vg, HD), _ptr(cos),
+                             _ptr(sin), cs, B, T, H, d, dtype_code(v.dtype), _ptr(k_out), _ptr(vt), ldv,
+                             _stream(v))
+    _check(st, "gsa_prologue_vt")
+    return k_out, vt
+
+
+def selection_mask(idx, Tkv: int, count=None, mask=None, out=None):
+    """uint32 bitmask [B,T,W] of the valid selected keys of every row."""
+    lib = load()
+    _need_cuda(idx, count, mask)
+    B, T, K = idx.shape
+    _expect(idx.dtype == torch.int32 and idx.stride(2) == 1, "idx: int32 with unit stride along k")
+    if count is not None:
+        _expect(tuple(count.shape) == (B, T) and count.dtype == torch.int32 and count.is_contiguous(),
+                "count: contiguous int32 [B,T]")
+    if mask is not None:
+        _expect(tuple(mask.shape) == tuple(idx.shape) and mask.stride() == idx.stride(), "mask: idx's layout")
+    W = mask_words(Tkv)
+    if out is None:
+        out = torch.empty(B, T, W, device=idx.device, dtype=torch.int32)
+    _expect(tuple(out.shape) == (B, T, W) and out.is_contiguous(), "bits: contiguous [B,T,W]")
+    st = lib.gsa_selection_mask(_ptr(idx), idx.stride(0), idx.stride(1), K, _ptr(count), _ptr(mask),
+                                B, T, Tkv, _ptr(out), out.stride(0), out.stride(1), _stream(idx))
+    _check(st, "gsa_selection_mask")
+    return out
+
+
+def dense_attn(q, k, vt, bits, scale: float, og=None, cos=None, sin=None, flags: int = 0,
+               causal: bool = True, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block-dense masked attention -> out [B,T,H,d] (bf16)."""
+    lib = load()
+    _need_cuda(q, k, vt, bits, og, cos, sin)
+    B, T, H, d = q.shape
+    Tkv = k.shape[1]
+    HD = H * d
+    _expect(k.shape[0] == B and tuple(k.shape[2:]) == (H, d) and k.dtype == q.dtype, "k: [B,Tkv,H,d]")
+    _expect(vt.dim() == 4 and tuple(vt.shape[:3]) == (B, H, d) and vt.shape[3] >= vt_len(Tkv)
+            and vt.stride(3) == 1 and vt.stride(2) == vt.shape[3] and vt.dtype == q.dtype,
+            "vt: [B,H,d,ldv] rows of ldv >= Tkv rounded up to 64")
+    _expect(tuple(bits.shape) == (B, T, mask_words(Tkv)) and bits.stride(2) == 1, "bits: [B,T,W]")
+    if og is not None:
+        _expect(tuple(og.shape) == (B, T, H, d) and og.dtype == q.dtype, "og: [B,T,H,d] in q's dtype")
+    if flags & ATTN_ROPE_Q:
+        _expect(cos is not None and sin is not None and cos.dim() == 2 and cos.shape[0] >= T
+                and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape)
+                and cos.dtype == sin.dtype == q.dtype and cos.stride(1) == 1 and sin.stride() == cos.stride(),
+                "cos/sin: [>=T, d] in q's dtype")
+    if out is None:
+        out = torch.empty(B, T, H, d, device=q.device, dtype=q.dtype)
+    _expect(tuple(out.shape) == (B, T, H, d) and out.dtype == q.dtype, "out: [B,T,H,d] in q's dtype")
+    os_ = _rows(og, HD) if og is not None else (0, 0)
+    cs = cos.stride(0) if cos is not None else 0
+    st = lib.gsa_dense_attn(_ptr(q), *_rows(q, HD), _ptr(k), *_rows(k, HD), _ptr(vt), vt.stride(0),
+                            vt.stride(1), vt.shape[3], _ptr(bits), bits.stride(0), bits.stride(1),
+                            _ptr(og), *os_, _ptr(cos), _ptr(sin), cs, _ptr(out), *_rows(out, HD),
+                            B, T, Tkv, H, d, float(scale), dtype_code(q.dtype), int(flags), int(bool(causal)),
+                            _stream(q))
+    _check(st, "gsa_dense_attn")
     return out

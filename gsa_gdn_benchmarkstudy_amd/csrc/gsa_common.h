@@ -7,6 +7,10 @@
 
 #include "../../include/gsa_hip.h"
 
+// Every product and sum rounds on its own (torch's rounding points); fused
+// multiply-adds are written explicitly where wanted.
+#pragma clang fp contract(off)
+
 namespace gsa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -114,6 +118,23 @@ __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 __device__ __forceinline__ int count_below(uint64_t mask) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// RoPE on one lane's 8 elements: x*cos + rotate_half(x)*sin, where
+// rotate_half takes element i+64 (negated) for i < 64 and element i-64 for
+// i >= 64 -- the value held by lane (li +/- 8) of the same 16-lane row.
+template <typename T>
+__device__ __forceinline__ void rope8(float (&x)[8], const float (&c)[8], const float (&s)[8], int li) {
+  float partner[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) partner[i] = row16_swap8(x[i]);
+  const float sign = li < 8 ? -1.f : 1.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = Elem<T>::rnd(x[i] * c[i]);
+    const float r = Elem<T>::rnd((sign * partner[i]) * s[i]);
+    x[i] = Elem<T>::rnd(a + r);
+  }
 }
 
 // Monotone map of an fp32 score to uint32: a > b  <=>  key(a) > key(b).

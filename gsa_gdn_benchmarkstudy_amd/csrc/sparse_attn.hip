@@ -17,23 +17,6 @@
 
 namespace gsa {
 
-// RoPE on one lane's 8 elements: x*cos + rotate_half(x)*sin, where
-// rotate_half takes element i+64 (negated) for i < 64 and element i-64 for
-// i >= 64 -- the value held by lane (li +/- 8) of the same 16-lane row.
-template <typename T>
-__device__ __forceinline__ void rope8(float (&x)[8], const float (&c)[8], const float (&s)[8], int li) {
-  float partner[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) partner[i] = row16_swap8(x[i]);
-  const float sign = li < 8 ? -1.f : 1.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float a = Elem<T>::rnd(x[i] * c[i]);
-    const float r = Elem<T>::rnd((sign * partner[i]) * s[i]);
-    x[i] = Elem<T>::rnd(a + r);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Producer: k_out = RoPE(k) and/or v_out = v * sigmoid(vg)  (block = 16*H threads)
 // ---------------------------------------------------------------------------

@@ -251,10 +251,14 @@ class GatedSparseAttention(nn.Module):
          output columns; the slices are strided views, never copied);
       2. indexer stream: gsa_indexer_select -- MFMA indexer fused with the
          exact top-k, writing ascending int32 indices and per-row counts
-         (the T x T score matrix is never stored);
-         current stream: gsa_prologue -- RoPE(k) and v * sigmoid(vg);
-      3. join, then gsa_sparse_attn -- RoPE(q), gather attention with online
-         softmax, output gate -- and the o_proj GEMM.
+         (the T x T score matrix is never stored) -- and, for the dense
+         attention, gsa_selection_mask (the selection as a bitmask);
+         current stream: RoPE(k) and v * sigmoid(vg) (gsa_prologue_vt, V
+         transposed, or gsa_prologue);
+      3. join, then the attention with RoPE(q) and the output gate fused --
+         gsa_dense_attn (bf16: MFMA over every causal key tile, masked to the
+         selection) or gsa_sparse_attn (per-row gather of the selected keys)
+         -- and the o_proj GEMM.
     """
 
     def __init__(self, hidden_size: int, num_heads: int, k_max: int = 4096, d_indexer: int = 64,
@@ -285,6 +289,10 @@ class GatedSparseAttention(nn.Module):
         total = sum(self._proj_sizes)
         self._fused_width = (total + FUSED_ALIGN - 1) // FUSED_ALIGN * FUSED_ALIGN
         self._indexer_stream: Optional[torch.cuda.Stream] = None
+        # Attention kernel: "dense" (block-dense MFMA over the causal key tiles
+        # with the selection as a bitmask, bf16), "gather" (per-row gather of
+        # the selected keys, bf16 and fp32), or "auto" (dense for bf16).
+        self.attn_impl = "auto"
         # Optional per-kernel timing hook: a list to which forward appends
         # (start, end) event pairs around the sparse-attention launch.
         self.attn_events: Optional[list] = None
@@ -353,6 +361,17 @@ class GatedSparseAttention(nn.Module):
         bias = self.indexer.idx_bias.detach().float().contiguous()
         return _abi.indexer_select(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale, k_eff)
 
+    def uses_dense(self, dtype: torch.dtype) -> bool:
+        if self.attn_impl not in ("auto", "dense", "gather"):
+            raise ValueError(f"attn_impl {self.attn_impl!r}: expected 'auto', 'dense' or 'gather'")
+        if self.attn_impl == "gather":
+            return False
+        if dtype != torch.bfloat16:
+            if self.attn_impl == "dense":
+                raise ValueError("the block-dense attention kernel is bf16 only")
+            return False
+        return True
+
     def forward(self, x: torch.Tensor, attention_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if not x.is_cuda:
             raise RuntimeError("GatedSparseAttention (HIP) needs a device tensor")
@@ -367,7 +386,9 @@ class GatedSparseAttention(nn.Module):
         views = self.project(x)
         _range_pop()
 
-        # Track A: indexer + top-k on the side stream
+        dense = self.uses_dense(x.dtype)
+
+        # Track A: indexer + top-k (+ its bitmask) on the side stream
         if self._indexer_stream is None or self._indexer_stream.device != dev:
             self._indexer_stream = torch.cuda.Stream(device=dev)
         side = self._indexer_stream
@@ -375,18 +396,23 @@ class GatedSparseAttention(nn.Module):
         with torch.cuda.stream(side):
             _range_push("gsa_hip/indexer_select")
             idx, cnt = self.select(views, T)
+            bits = _abi.selection_mask(idx, T, count=cnt) if dense else None
             _range_pop()
 
         # Track B: RoPE(k) and the value gate on the current stream
         _range_push("gsa_hip/prologue")
         cos, sin = self.rotary_emb(T, dev, x.dtype)
         cos, sin = cos.contiguous(), sin.contiguous()
-        k_rope, v_gated = _abi.prologue(k=views["k"], v=views["v"], vg=views["vg"], cos=cos, sin=sin)
+        if dense:
+            k_rope, v_gated = _abi.prologue_vt(views["v"], views["vg"], k=views["k"], cos=cos, sin=sin)
+        else:
+            k_rope, v_gated = _abi.prologue(k=views["k"], v=views["v"], vg=views["vg"], cos=cos, sin=sin)
         _range_pop()
 
         cur.wait_stream(side)
-        idx.record_stream(cur)
-        cnt.record_stream(cur)
+        for t in (idx, cnt, bits):
+            if t is not None:
+                t.record_stream(cur)
         views["_buf"].record_stream(side)
 
         _range_push("gsa_hip/sparse_attn")
@@ -394,9 +420,13 @@ class GatedSparseAttention(nn.Module):
         if self.attn_events is not None:
             ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             ev[0].record(cur)
-        attn = _abi.sparse_attn(views["q"], k_rope, v_gated, idx, self.scale, count=cnt,
-                                og=views["og"], cos=cos, sin=sin,
-                                flags=_abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE)
+        flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
+        if dense:
+            attn = _abi.dense_attn(views["q"], k_rope, v_gated, bits, self.scale, og=views["og"],
+                                   cos=cos, sin=sin, flags=flags, causal=True)
+        else:
+            attn = _abi.sparse_attn(views["q"], k_rope, v_gated, idx, self.scale, count=cnt,
+                                    og=views["og"], cos=cos, sin=sin, flags=flags)
         if ev is not None:
             ev[1].record(cur)
             self.attn_events.append(ev)

@@ -162,6 +162,57 @@ int gsa_sparse_attn(const void* q, int64_t q_sb, int64_t q_st,
                     int dtype, int flags,
                     void* stream);
 
+/*
+ * Producer for the block-dense attention: RoPE on k (k == NULL skips it) and
+ * the G2 gate with V written transposed.  Replaces gsa_triton/gsa_opt.py:
+ * 685-697 like gsa_prologue, with the value output laid out for
+ * gsa_dense_attn: vt[b][h][d][j] = (v * sigmoid(vg))[b][j][h][d] for
+ * j < T, 0 for T <= j < ldv (ldv a multiple of 64, >= T).  bf16 only.
+ * k_out contiguous [B,T,H,d]; vt contiguous [B,H,d,ldv].
+ */
+int gsa_prologue_vt(const void* k, int64_t k_sb, int64_t k_st,
+                    const void* v, int64_t v_sb, int64_t v_st,
+                    const void* vg, int64_t g_sb, int64_t g_st,
+                    const void* cos, const void* sin, int64_t cs_st,
+                    int B, int T, int H, int d, int dtype,
+                    void* k_out, void* vt, int ldv,
+                    void* stream);
+
+/*
+ * Selection bitmask: bits[b][t][j/32] bit j%32 is set when key j is a valid
+ * selected entry of row (b,t) -- entry m valid as in gsa_sparse_attn (m <
+ * count, mask != 0), index clamped to [0, Tkv-1] like the reference
+ * (gsa_triton/gsa_ref.py:196); a key selected twice is set once.
+ * bits uint32 [B,T,W] with W = 2*ceil(Tkv/64) (8-byte aligned rows).
+ * Replaces nothing in the reference: it is the mask form of the selection
+ * (gsa_opt.py:671-677) that gsa_dense_attn consumes.
+ */
+int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel,
+                       const int32_t* count, const uint8_t* mask,
+                       int B, int T, int Tkv, uint32_t* bits, int64_t b_sb, int64_t b_st,
+                       void* stream);
+
+/*
+ * Block-dense sparse attention on MFMA: the function of gsa_sparse_attn
+ * (fused_sparse_attention, gsa_triton/gsa_opt.py:349-383, with the optional
+ * RoPE(q) and G1 gate of gsa_opt.py:692-701,719-721) computed over whole
+ * 64-key tiles with the selection applied as a bitmask (gsa_selection_mask).
+ * q, out, og [B,T,H,d]; k [B,Tkv,H,d] (RoPE'd); vt [B,H,d,ldv] as written by
+ * gsa_prologue_vt (strides vt_sb, vt_sh per batch and head; rows of ldv).
+ * causal != 0: key tiles after a 64-row query block's last row are skipped
+ * (the selection must then be causal).  bf16 only; d == 128, 1 <= H <= 64.
+ */
+int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
+                   const void* k, int64_t k_sb, int64_t k_st,
+                   const void* vt, int64_t vt_sb, int64_t vt_sh, int ldv,
+                   const uint32_t* bits, int64_t b_sb, int64_t b_st,
+                   const void* og, int64_t o_sb, int64_t o_st,
+                   const void* cos, const void* sin, int64_t cs_st,
+                   void* out, int64_t out_sb, int64_t out_st,
+                   int B, int T, int Tkv, int H, int d, float scale,
+                   int dtype, int flags, int causal,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,6 +7,7 @@ producer matches the oracle's op-by-op bf16 rounding; attention within one
 bf16 rounding (bf16) or 1e-5 (fp32) of a float64 evaluation.
 """
 
+import math
 import os
 
 import numpy as np
@@ -251,3 +252,97 @@ def test_sparse_attention_fused_rope_gate_count(dev, dtype):
     else:
         ref = att * torch.sigmoid(og.double())
         assert torch.allclose(out.double(), ref, atol=1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# block-dense attention path
+# ---------------------------------------------------------------------------
+
+def test_prologue_vt_matches_prologue(dev):
+    B, T, H = 2, 100, 4
+    _log("prologue_vt")
+    g = torch.Generator().manual_seed(11)
+    k = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16).to(dev)
+    vg = (torch.randn(B, T, H, 128, generator=g) * 3).to(torch.bfloat16).to(dev)
+    cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
+    cos, sin = cos.to(dev), sin.to(dev)
+    ko, vo = _abi.prologue(k=k, v=v, vg=vg, cos=cos, sin=sin)
+    ko2, vt = _abi.prologue_vt(v, vg, k=k, cos=cos, sin=sin)
+    assert vt.shape == (B, H, 128, 128)
+    assert torch.equal(ko.cpu(), ko2.cpu())
+    assert torch.equal(vt[..., :T].cpu(), vo.permute(0, 2, 3, 1).cpu())
+    assert torch.all(vt[..., T:].cpu() == 0)
+
+
+def test_selection_mask_bits(dev):
+    B, T, k = 2, 130, 20
+    _log("selection_mask")
+    s = _tie_scores(B, T, 1000, seed=3)
+    ia, cnt = orc.select_ascending(s, k)
+    bits = _abi.selection_mask(ia.to(dev), T, count=cnt.to(dev)).cpu()
+    assert bits.shape == (B, T, 2 * ((T + 63) // 64))
+    words = bits.numpy().view(np.uint32)
+    for b in range(B):
+        for t in range(T):
+            got = {w * 32 + i for w in range(words.shape[2]) for i in range(32) if (words[b, t, w] >> i) & 1}
+            assert got == set(ia[b, t, :cnt[b, t]].tolist())
+
+
+def _dense_case(B, T, H, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    kk = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    og = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    s = torch.rand(B, T, T, generator=g).masked_fill(
+        torch.triu(torch.ones(T, T, dtype=torch.bool), 1), float("-inf"))
+    ia, cnt = orc.select_ascending(s, k)
+    return q, kk, v, og, ia, cnt
+
+
+@pytest.mark.parametrize("B,T,H,k", [(1, 64, 16, 16), (2, 100, 4, 37), (1, 300, 2, 100), (1, 1030, 16, 256)])
+def test_dense_attention_vs_oracle_and_gather(dev, B, T, H, k):
+    _log(f"dense_attn B={B} T={T} H={H} k={k}")
+    q, kk, v, og, ia, cnt = _dense_case(B, T, H, k, seed=T + H)
+    cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
+    qd, kd, vd, ogd, iad, cntd = (t.to(dev) for t in (q, kk, v, og, ia, cnt))
+    cosd, sind = cos.to(dev), sin.to(dev)
+    ldv = _abi.vt_len(T)
+    vt = torch.zeros(B, H, 128, ldv, dtype=torch.bfloat16, device=dev)
+    vt[..., :T] = vd.permute(0, 2, 3, 1)
+    bits = _abi.selection_mask(iad, T, count=cntd)
+    flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
+    dense = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, og=ogd, cos=cosd, sin=sind, flags=flags).cpu()
+    gather = _abi.sparse_attn(qd, kd, vd, iad, 128 ** -0.5, count=cntd, og=ogd, cos=cosd, sin=sind,
+                              flags=flags).cpu()
+    qr = orc.apply_rope(q, cos[None, :, None], sin[None, :, None])
+    mask = torch.arange(k)[None, None, :] < cnt[..., None]
+    att = orc.sparse_attention(qr.double(), kk.double(), v.double(), ia, mask, 128 ** -0.5)
+    ref = (att.to(torch.bfloat16) * torch.sigmoid(og)).double()
+    for name, out in (("dense", dense), ("gather", gather)):
+        diff = (out.double() - ref).abs()
+        rel = (torch.linalg.vector_norm(out.double() - ref) / torch.linalg.vector_norm(ref)).item()
+        _log(f"  {name}: rel-L2 {rel:.2e} max|diff| {diff.max().item():.2e}")
+        # P is rounded to bf16 before the P.V product in the dense kernel: allow
+        # two output ulps plus a 2^-9 perturbation of the weights
+        assert torch.all(diff <= ref.abs() * 2 ** -6 + 2e-3 * v.abs().max().item() / math.sqrt(k) + 1e-6)
+        assert rel < 5e-3
+
+
+def test_dense_attention_noncausal_selection(dev):
+    """A selection with keys after the query (non-causal) is honoured with causal=False."""
+    B, T, H, k = 1, 128, 2, 8
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    kk = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    s = torch.rand(B, T, T, generator=g)
+    ia, cnt = orc.select_ascending(s, k)
+    vt = torch.zeros(B, H, 128, 128, dtype=torch.bfloat16)
+    vt[..., :T] = v.permute(0, 2, 3, 1)
+    bits = _abi.selection_mask(ia.to(dev), T, count=cnt.to(dev))
+    out = _abi.dense_attn(q.to(dev), kk.to(dev), vt.to(dev), bits, 0.1, causal=False).cpu()
+    mask = torch.arange(k)[None, None, :] < cnt[..., None]
+    ref = orc.sparse_attention(q.double(), kk.double(), v.double(), ia, mask, 0.1)
+    assert (torch.linalg.vector_norm(out.double() - ref) / torch.linalg.vector_norm(ref)).item() < 5e-3

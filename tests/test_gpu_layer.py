@@ -31,9 +31,10 @@ def _log(msg):
     print(msg, flush=True)
 
 
-def _model(cfg, sd, dev, dtype):
+def _model(cfg, sd, dev, dtype, impl="auto"):
     m = GatedSparseAttention(cfg.hidden_size, cfg.num_heads, k_max=cfg.k_max, d_indexer=cfg.d_indexer,
                              n_idx_heads=cfg.n_idx_heads, k_base=cfg.k_base, k_min=cfg.k_min)
+    m.attn_impl = impl
     m = m.to(dev).to(dtype).eval()
     m.load_state_dict({k: v.to(dev) for k, v in sd.items()}, strict=True)
     m.fuse_projections()
@@ -89,17 +90,20 @@ GOLDEN = {
 }
 
 
+@pytest.mark.parametrize("impl", ["dense", "gather"])
 @pytest.mark.parametrize("name", sorted(GOLDEN))
-def test_golden_fixture(dev, name):
-    _log(f"golden {name}")
+def test_golden_fixture(dev, name, impl):
+    _log(f"golden {name} impl={impl}")
     dt_name, kw, wseed = GOLDEN[name]
     dt = getattr(torch, dt_name)
+    if impl == "dense" and dt != torch.bfloat16:
+        pytest.skip("the block-dense attention is bf16 only")
     z = np.load(os.path.join(GOLDEN_DIR, f"{name}.npz"))
     cfg = orc.GSAConfig(**kw)
     sd = orc.cast_state(orc.synthetic_state(cfg, seed=wseed), dt)
     assert make_golden.weights_digest(sd) == str(z["wdigest"]), "fixture weights no longer regenerate: rerun make_golden.py"
     x = torch.from_numpy(z["x"]).to(dt)
-    m = _model(cfg, sd, dev, dt)
+    m = _model(cfg, sd, dev, dt, impl)
     with torch.no_grad():
         y = m(x.to(dev)).cpu()
     idx, cnt = _gpu_selection(m, x.to(dev))
@@ -121,14 +125,15 @@ def test_golden_fixture(dev, name):
 # oracle comparisons at growing sizes
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype,impl", [(torch.bfloat16, "dense"), (torch.bfloat16, "gather"),
+                                        (torch.float32, "gather")])
 @pytest.mark.parametrize("B,T", [(1, 256), (2, 200)])
-def test_layer_vs_oracle_small(dev, dtype, B, T):
-    _log(f"layer small dtype={dtype} B={B} T={T}")
+def test_layer_vs_oracle_small(dev, dtype, impl, B, T):
+    _log(f"layer small dtype={dtype} impl={impl} B={B} T={T}")
     cfg = orc.GSAConfig(hidden_size=512, num_heads=4, k_max=96, k_base=64, k_min=16)
     sd = orc.cast_state(orc.synthetic_state(cfg, seed=7), dtype)
     x = orc.synthetic_input(B, T, cfg.hidden_size, seed=8).to(dtype)
-    m = _model(cfg, sd, dev, dtype)
+    m = _model(cfg, sd, dev, dtype, impl)
     with torch.no_grad():
         y = m(x.to(dev)).cpu()
     if dtype == torch.float32:
@@ -163,19 +168,36 @@ def test_layer_c1_fp32(dev):
     assert torch.allclose(y, ref, atol=1e-4, rtol=0)
 
 
-def test_layer_c2_bf16_sampled_rows(dev):
+@pytest.mark.parametrize("impl", ["dense", "gather"])
+def test_layer_c2_bf16_sampled_rows(dev, impl):
     """configs[1] shape: T=4096, D=2048, bf16, k=2048 -- oracle on sampled row blocks."""
-    _log("layer c2 bf16 T=4096 (sampled rows)")
+    _log(f"layer c2 bf16 T=4096 (sampled rows) impl={impl}")
     cfg = orc.GSAConfig(hidden_size=2048, num_heads=16, k_max=4096, k_base=2048, k_min=256)
     sd = orc.cast_state(orc.synthetic_state(cfg, seed=0), torch.bfloat16)
     x = orc.synthetic_input(1, 4096, 2048, seed=1).to(torch.bfloat16)
-    m = _model(cfg, sd, dev, torch.bfloat16)
+    m = _model(cfg, sd, dev, torch.bfloat16, impl)
     with torch.no_grad():
         y = m(x.to(dev)).cpu()
     p = orc.project(sd, cfg, x)
     for r0 in (0, 1500, 2040, 4064):
         ref = orc.attend_rows(sd, cfg, p, r0, r0 + 32)
         _check_bf16(y[:, r0:r0 + 32], ref, rel_l2=3e-2)
+
+
+def test_layer_dense_equals_gather_c2_shape(dev):
+    """Both attention kernels on the same layer and input: same selection, outputs
+    within bf16 rounding of each other."""
+    cfg = orc.GSAConfig(hidden_size=2048, num_heads=16, k_max=4096, k_base=2048, k_min=256)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=3), torch.bfloat16)
+    x = orc.synthetic_input(1, 4096, 2048, seed=4).to(torch.bfloat16).to(dev)
+    m = _model(cfg, sd, dev, torch.bfloat16, "gather")
+    with torch.no_grad():
+        yg = m(x)
+        m.attn_impl = "dense"
+        yd = m(x)
+    rel = (torch.linalg.vector_norm((yd - yg).float()) / torch.linalg.vector_norm(yg.float())).item()
+    _log(f"  dense vs gather rel-L2 {rel:.2e}")
+    assert rel < 1e-2
 
 
 def test_layer_repeat_is_deterministic(dev):
