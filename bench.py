@@ -204,7 +204,7 @@ def main():
         e0.record()
         n_idx = 5
         for _ in range(n_idx):
-            model.select(views, T)
+            model.select(views, T, indices=not model.uses_dense(dtype))
         e1.record()
         torch.cuda.synchronize()
         idx_ms = e0.elapsed_time(e1) / n_idx

@@ -45,7 +45,7 @@ _PROTOS = {
                             _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp], _i32),
     "gsa_topk_select": ([_vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "gsa_indexer_select": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
-                            _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
+                            _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _vp], _i32),
     "gsa_prologue": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
                       _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
     "gsa_sparse_attn": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
@@ -175,9 +175,14 @@ def topk_select(scores: torch.Tensor, k_eff: int, order: int = ORDER_INDEX_ASC,
     return idx, cnt, mask
 
 
-def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int,
-                   idx: Optional[torch.Tensor] = None, cnt: Optional[torch.Tensor] = None):
-    """Fused indexer + top-k -> (idx int32 [B,T,k_eff] ascending, count int32 [B,T])."""
+def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int, indices: bool = True,
+                   bits: Optional[torch.Tensor] = None):
+    """Fused indexer + exact top-k.
+
+    Returns (bits, idx, count): the selection bitmask int32 [B,T,W] (W =
+    2*ceil(T/64)) and, when ``indices``, ascending int32 indices [B,T,k_eff]
+    and counts int32 [B,T] (else None, None).
+    """
     lib = load()
     _need_cuda(q_idx, k_idx, w, bias32)
     B, T, Hi, di = q_idx.shape
@@ -185,20 +190,20 @@ def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int,
     _expect(tuple(w.shape) == (B, T, Hi), f"w {tuple(w.shape)} != {(B, T, Hi)}")
     _expect(bias32.dtype == torch.float32 and bias32.numel() == Hi and bias32.is_contiguous(), "bias: fp32 [Hi]")
     _expect(k_idx.dtype == q_idx.dtype == w.dtype, "q_idx, k_idx, w must share a dtype")
-    if idx is None:
+    W = mask_words(T)
+    if bits is None:
+        bits = torch.empty(B, T, W, device=q_idx.device, dtype=torch.int32)
+    _expect(tuple(bits.shape) == (B, T, W) and bits.is_contiguous(), "bits: contiguous [B,T,W]")
+    idx = cnt = None
+    if indices:
         idx = torch.empty(B, T, k_eff, device=q_idx.device, dtype=torch.int32)
-    if cnt is None:
         cnt = torch.empty(B, T, device=q_idx.device, dtype=torch.int32)
-    _expect(tuple(idx.shape) == (B, T, k_eff) and idx.dtype == torch.int32 and idx.is_contiguous(),
-            "idx: contiguous int32 [B,T,k_eff]")
-    _expect(tuple(cnt.shape) == (B, T) and cnt.dtype == torch.int32 and cnt.is_contiguous(),
-            "count: contiguous int32 [B,T]")
     qs, ks, ws = _rows(q_idx, Hi * di), _rows(k_idx, di), _rows(w, Hi)
     st = lib.gsa_indexer_select(_ptr(q_idx), *qs, _ptr(k_idx), *ks, _ptr(w), *ws, _ptr(bias32),
                                 float(scale), B, T, Hi, di, int(k_eff), dtype_code(q_idx.dtype),
-                                _ptr(idx), _ptr(cnt), _stream(q_idx))
+                                _ptr(bits), bits.stride(0), bits.stride(1), _ptr(idx), _ptr(cnt), _stream(q_idx))
     _check(st, "gsa_indexer_select")
-    return idx, cnt
+    return bits, idx, cnt
 
 
 def prologue(k=None, v=None, vg=None, cos=None, sin=None, k_out=None, v_out=None):

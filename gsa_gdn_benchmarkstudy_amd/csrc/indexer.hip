@@ -179,162 +179,183 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 // ---------------------------------------------------------------------------
 // Fused indexer + exact top-k (never stores the score matrix).
 //
-// One wave per 16-row group, heaviest groups first.  Rows with t+1 <= k
-// select every causal key.  For the other rows the scores are recomputed in
-// passes over the causal key tiles:
-//   1. HIST   histogram of value-linear bins  bin = floor(s * NB / sum_h a_h)
-//             -> the bin b1 holding the k-th largest score, and how many of
-//             the bin's entries are still needed.
-//   2. COLLECT keys of the entries in bin b1 (at most kCap) -> exact radix
-//             select among them -> threshold key theta and the number of
-//             entries equal to theta to take (lowest indices first).
-//      DIGIT  (only when a bin overflows kCap): four 8-bit radix passes over
-//             the keys in bin b1 replace COLLECT.
-//   3. EMIT   entries with key > theta, plus the first tie_need entries with
-//             key == theta, written in ascending key-index order.
+// Output: the selection as a bitmask, bits[b][t] bit j set iff key j is one
+// of row t's selected keys (W = 2*ceil(T/64) uint32 words per row; words past
+// row t's causal range are zero).  One 256-thread block per 16-row group,
+// heaviest groups first; its 4 waves take the group's causal 16-key tiles
+// round-robin and share the row state in LDS.  Rows with t+1 <= k select
+// every causal key.  For the others the scores are computed twice:
+//   pass 1  value-linear histogram, bin = floor(s * NB / sum_h sigmoid(w_h))
+//           -> the bin b1 holding the k-th largest score and the rank of the
+//           k-th largest inside it;
+//   pass 2  entries in bins above b1 are selected: ballot -> one 16-bit chunk
+//           of the row's bitmask per 16-key tile; entries in b1 (at most
+//           kCap per row) are collected as (key, index);
+//   resolve exact MSB-first radix select among a row's candidates -> the
+//           threshold key theta and how many entries equal to theta to take,
+//           lowest indices first; winning candidates are OR-ed into the mask.
+// A bin holding more than kCap entries (degenerate scores, e.g. all equal)
+// falls back to four 8-bit radix passes over the bin, then one ordered pass
+// by a single wave marks the winners.
 // ---------------------------------------------------------------------------
-constexpr int kNB = 256;
-constexpr int kCap = 256;
-constexpr int kLdsStride = kNB + 1;   // odd stride: rows of one bin in distinct banks
+constexpr int kNB = 512;                 // histogram bins per row
+constexpr int kCap = 512;                // candidates per row
+constexpr int kHStride = kNB + 1;        // odd stride: one bin of 16 rows in distinct banks
+constexpr int kGroupWaves = 4;
 
-enum RowMode : int { kTrivial = 0, kActive = 1, kResolved = 2, kOverflow = 3 };
+enum RowMode : int { kNone = 0, kTrivial = 1, kActive = 2, kResolved = 3, kOverflow = 4 };
 
 __device__ __forceinline__ int bin_of(float s, float inv_w) {
   return (int)fmaxf(0.f, fminf(s * inv_w, (float)(kNB - 1)));
 }
 
+// Causal-prefix chunk of row `row` for 16-key tile `tile`: keys <= row set.
+__device__ __forceinline__ uint16_t prefix_chunk(int row, int tile) {
+  const int n = row - 16 * tile + 1;    // keys of this tile at or before the row
+  return n >= 16 ? (uint16_t)0xffffu : (n <= 0 ? (uint16_t)0 : (uint16_t)((1u << n) - 1u));
+}
+
 template <typename T>
-__global__ __launch_bounds__(64) void indexer_select_kernel(IdxArgs p, int k_eff, int32_t* idx_out,
-                                                            int32_t* count_out) {
-  __shared__ uint32_t sh[16 * kLdsStride];   // histogram bins, or candidate keys
+__global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff, uint32_t* bits,
+                                                           int64_t b_sb, int64_t b_st) {
+  __shared__ uint32_t sh[16 * kHStride];   // histogram, then candidate keys
+  __shared__ uint32_t sh_idx[16 * kCap];   // candidate key indices
   __shared__ uint32_t sh_cnt[16];
   __shared__ int st_mode[16], st_b1[16], st_need[16];
-  __shared__ uint32_t st_key[16];            // radix prefix, then theta
+  __shared__ uint32_t st_key[16];
+  __shared__ int st_any[2];                // [0] any active row, [1] any overflow
 
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, lr = lane & 15;
   const int ngroups = (p.T + 15) >> 4;
   const int b = blockIdx.x % p.B;
-  const int r0 = (ngroups - 1 - blockIdx.x / p.B) * 16;
-  const int64_t out_row0 = (int64_t)b * p.T;
+  const int rg_idx = ngroups - 1 - blockIdx.x / p.B;
+  const int r0 = rg_idx * 16;
+  uint32_t* bbase = bits + b * b_sb;
+  uint16_t* b16 = reinterpret_cast<uint16_t*>(bbase);
+  const int64_t row16 = 2 * b_st;          // uint16 chunks per row
 
-  // Row classification (lane < 16 owns row r0 + lane).
-  if (lane < 16) {
-    const int row = r0 + lane;
-    st_mode[lane] = (row < p.T && row + 1 > k_eff) ? kActive : kTrivial;
-    st_need[lane] = k_eff;
+  if (tid < 16) {
+    const int row = r0 + tid;
+    st_mode[tid] = row >= p.T ? kNone : (row + 1 > k_eff ? kActive : kTrivial);
+    st_need[tid] = k_eff;
+    sh_cnt[tid] = 0u;
+  }
+  if (tid < 2) st_any[tid] = 0;
+  __syncthreads();
+  if (tid < 16 && st_mode[tid] == kActive) st_any[0] = 1;
+
+  // Chunks of tile rg_idx+1 .. end of the 64-key tile are zero for every row;
+  // trivial rows get their causal prefix now.
+  const int ntl = rg_idx + 1;                  // causal 16-key tiles 0 .. rg_idx
+  const int zend = (rg_idx | 3) + 1;
+  for (int i = tid; i < 16 * zend; i += 256) {
+    const int rl = i / zend, tile = i % zend;
+    const int row = r0 + rl;
+    if (row >= p.T) continue;
+    if (tile >= ntl) b16[row * row16 + tile] = 0;
+    else if (st_mode[rl] == kTrivial) b16[row * row16 + tile] = prefix_chunk(row, tile);
   }
   __syncthreads();
+  if (!st_any[0]) return;
 
-  // Trivial rows: every causal key, then t+1, t+2, ... (the lowest-index
-  // invalid entries), i.e. the row is 0..k_eff-1 with count t+1.
-  bool any_active = false;
-  for (int rl = 0; rl < 16; ++rl) {
-    const int row = r0 + rl;
-    if (row >= p.T) break;
-    if (st_mode[rl] == kActive) { any_active = true; continue; }
-    int32_t* orow = idx_out + (out_row0 + row) * k_eff;
-    for (int m = lane; m < k_eff; m += 64) orow[m] = m;
-    if (lane == 0) count_out[out_row0 + row] = row + 1;
-  }
-  if (!any_active) return;
-
-  RowGroup<T> rg;
-  rg.init(p, b, r0, lane);
-  int mode[4], b1[4], need[4];
+  RowGroup<T> rgp;
+  rgp.init(p, b, r0, lane);
+  int mode[4], b1[4];
   float inv_w[4];
-  uint32_t theta[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int rl = 4 * g + e;
-    mode[e] = st_mode[rl];
-    need[e] = k_eff;
-    const float smax = ((rg.a[e][0] + rg.a[e][1]) + rg.a[e][2]) + rg.a[e][3];
+    mode[e] = st_mode[4 * g + e];
+    const float smax = ((rgp.a[e][0] + rgp.a[e][1]) + rgp.a[e][2]) + rgp.a[e][3];
     inv_w[e] = (float)kNB / (smax * 1.0009765625f + 1e-30f);
     b1[e] = 0;
-    theta[e] = 0;
   }
-  const int ntl = (r0 >> 4) + 1;   // causal key tiles 0 .. r0/16
 
   typename Mfma<T>::Op kb[Mfma<T>::kSteps], kn[Mfma<T>::kSteps];
-
-  // Visit every causal (row, key) of the group; f(e, row, col, score) runs on
-  // entries of active rows.
+  // This wave's tiles: wave, wave+4, ...; f(e, row, col, tile, valid, score).
   auto sweep = [&](auto&& f) {
-    rg.load_keys(0, p.T, lane, kn);
-    for (int t = 0; t < ntl; ++t) {
-      const int j0 = t * 16;
+    int t = wave;
+    if (t < ntl) rgp.load_keys(t * 16, p.T, lane, kn);
+    for (; t < ntl; t += kGroupWaves) {
 #pragma unroll
       for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = kn[s];
-      if (t + 1 < ntl) rg.load_keys(j0 + 16, p.T, lane, kn);
+      if (t + kGroupWaves < ntl) rgp.load_keys((t + kGroupWaves) * 16, p.T, lane, kn);
       floatx4 acc[kHi];
-      rg.mma(kb, acc);
-      const int col = j0 + lr;
+      rgp.mma(kb, acc);
+      const int col = t * 16 + lr;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = r0 + 4 * g + e;
-        const bool valid = (mode[e] != kTrivial) && col <= row;   // row < T for non-trivial
-        f(e, row, col, valid, valid ? rg.score(acc, e) : 0.f);
+        const bool valid = mode[e] == kActive && col <= row;
+        f(e, row, col, t, valid, valid ? rgp.score(acc, e) : 0.f);
       }
     }
   };
 
-  auto zero_sh = [&]() {
-    for (int i = lane; i < 16 * kLdsStride; i += 64) sh[i] = 0u;
-    if (lane < 16) sh_cnt[lane] = 0u;
-    __syncthreads();
-  };
-
-  // Lane rl < 16: scan row rl's histogram from the top for the bin holding
-  // the need-th largest entry.  Returns the bin; need becomes the rank
-  // inside that bin.
-  auto scan_row = [&](int rl, int& nd) -> int {
+  auto scan_row = [&](int rl, int& nd) -> int {     // top-down cumulative search
     int cum = 0, bsel = 0;
     for (int bin = kNB - 1; bin >= 0; --bin) {
-      const int c = (int)sh[rl * kLdsStride + bin];
+      const int c = (int)sh[rl * kHStride + bin];
       if (cum + c >= nd) { bsel = bin; break; }
       cum += c;
     }
     nd -= cum;
     return bsel;
   };
+  auto zero_hist = [&]() {
+    for (int i = tid; i < 16 * kHStride; i += 256) sh[i] = 0u;
+    __syncthreads();
+  };
 
-  // ---- pass 1: value-linear histogram ------------------------------------
-  zero_sh();
-  sweep([&](int e, int, int, bool valid, float s) {
-    if (valid) atomicAdd(&sh[(4 * g + e) * kLdsStride + bin_of(s, inv_w[e])], 1u);
+  // ---- pass 1: histogram ---------------------------------------------------
+  zero_hist();
+  sweep([&](int e, int, int, int, bool valid, float s) {
+    if (valid) atomicAdd(&sh[(4 * g + e) * kHStride + bin_of(s, inv_w[e])], 1u);
   });
   __syncthreads();
-  if (lane < 16 && st_mode[lane] == kActive) {
-    int nd = st_need[lane];
-    st_b1[lane] = scan_row(lane, nd);
-    st_need[lane] = nd;
+  if (tid < 16 && st_mode[tid] == kActive) {
+    int nd = st_need[tid];
+    st_b1[tid] = scan_row(tid, nd);
+    st_need[tid] = nd;
   }
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < 4; ++e) { b1[e] = st_b1[4 * g + e]; need[e] = st_need[4 * g + e]; }
+  for (int e = 0; e < 4; ++e) b1[e] = st_b1[4 * g + e];
+  __syncthreads();   // sh is reused for candidate keys below
 
-  // ---- pass 2: collect the keys of bin b1 --------------------------------
-  zero_sh();
-  sweep([&](int e, int, int, bool valid, float s) {
-    if (valid && bin_of(s, inv_w[e]) == b1[e]) {
+  // ---- pass 2: bins above b1 -> mask chunks; bin b1 -> candidates ------------
+  sweep([&](int e, int row, int col, int t, bool valid, float s) {
+    const int bn = bin_of(s, inv_w[e]);
+    const bool sel = valid && bn > b1[e];
+    if (valid && bn == b1[e]) {
       const int rl = 4 * g + e;
       const uint32_t pos = atomicAdd(&sh_cnt[rl], 1u);
-      if (pos < (uint32_t)kCap) sh[rl * kLdsStride + pos] = score_key(s);
+      if (pos < (uint32_t)kCap) {
+        sh[rl * kHStride + pos] = score_key(s);
+        sh_idx[rl * kCap + pos] = (uint32_t)col;
+      }
     }
+    const uint64_t m = ballot64(sel);
+    if (lr == 0 && mode[e] == kActive) b16[row * row16 + t] = (uint16_t)(m >> (16 * g));
   });
+  __threadfence();
   __syncthreads();
-  // Exact radix select among the candidates, one row at a time across the wave.
-  bool any_overflow = false;
-  for (int rl = 0; rl < 16; ++rl) {
+
+  // ---- resolve: wave w takes rows 4w .. 4w+3 ----------------------------------
+  for (int q = 0; q < 4; ++q) {
+    const int rl = 4 * wave + q;
     if (st_mode[rl] != kActive) continue;
     const int n = (int)sh_cnt[rl];
-    if (n > kCap) { any_overflow = true; continue; }
-    uint32_t cv[kCap / 64];
+    if (n > kCap) {
+      if (lane == 0) { st_mode[rl] = kOverflow; st_any[1] = 1; }
+      continue;
+    }
+    uint32_t cv[kCap / 64], ci[kCap / 64];
 #pragma unroll
     for (int i = 0; i < kCap / 64; ++i) {
-      const int idx = i * 64 + lane;
-      cv[i] = idx < n ? sh[rl * kLdsStride + idx] : 0u;
+      const int c = i * 64 + lane;
+      cv[i] = c < n ? sh[rl * kHStride + c] : 0u;
+      ci[i] = c < n ? sh_idx[rl * kCap + c] : 0u;
     }
     int k = st_need[rl];
     uint32_t prefix = 0u, pmask = 0u;
@@ -342,75 +363,144 @@ __global__ __launch_bounds__(64) void indexer_select_kernel(IdxArgs p, int k_eff
       const uint32_t tm = pmask | (1u << bit), tv = prefix | (1u << bit);
       int c = 0;
 #pragma unroll
-      for (int i = 0; i < kCap / 64; ++i)
-        c += __popcll(ballot64((i * 64 + lane) < n && (cv[i] & tm) == tv));
+      for (int i = 0; i < kCap / 64; ++i) c += __popcll(ballot64((i * 64 + lane) < n && (cv[i] & tm) == tv));
       if (c >= k) prefix = tv; else k -= c;
       pmask = tm;
     }
-    if (lane == 0) { st_key[rl] = prefix; st_need[rl] = k; st_mode[rl] = kResolved; }
+    // winners: key > theta, or key == theta among the k lowest indices of the ties
+    const int row = r0 + rl;
+    uint32_t* brow = bbase + (int64_t)row * b_st;
+#pragma unroll
+    for (int i = 0; i < kCap / 64; ++i) {
+      const int c = i * 64 + lane;
+      if (c >= n) continue;
+      bool win = cv[i] > prefix;
+      if (cv[i] == prefix) {
+        int rank = 0;
+        for (int o = 0; o < n; ++o)
+          rank += (sh[rl * kHStride + o] == prefix && sh_idx[rl * kCap + o] < ci[i]) ? 1 : 0;
+        win = rank < k;
+      }
+      if (win) atomicOr(&brow[ci[i] >> 5], 1u << (ci[i] & 31));
+    }
   }
   __syncthreads();
+  if (!st_any[1]) return;
 
-  // ---- DIGIT passes: rows whose bin overflowed ----------------------------
-  if (any_overflow) {
-    if (lane < 16 && st_mode[lane] == kActive) { st_mode[lane] = kOverflow; st_key[lane] = 0u; }
-    __syncthreads();
+  // ---- overflow rows: radix passes over the keys of bin b1 --------------------
+  if (tid < 16 && st_mode[tid] == kOverflow) st_key[tid] = 0u;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) { mode[e] = st_mode[4 * g + e]; need[e] = st_need[4 * g + e]; }
-    for (int level = 0; level < 4; ++level) {
-      uint32_t pre[4];
+  for (int e = 0; e < 4; ++e) mode[e] = st_mode[4 * g + e] == kOverflow ? kActive : kNone;
+  for (int level = 0; level < 4; ++level) {
+    uint32_t pre[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pre[e] = st_key[4 * g + e];
-      const int hi_shift = 32 - 8 * level, lo_shift = 24 - 8 * level;
-      zero_sh();
-      sweep([&](int e, int, int, bool valid, float s) {
-        if (valid && mode[e] == kOverflow && bin_of(s, inv_w[e]) == b1[e]) {
-          const uint32_t key = score_key(s);
-          if (level == 0 || (key >> hi_shift) == pre[e])
-            atomicAdd(&sh[(4 * g + e) * kLdsStride + ((key >> lo_shift) & 255u)], 1u);
-        }
-      });
-      __syncthreads();
-      if (lane < 16 && st_mode[lane] == kOverflow) {
-        int nd = st_need[lane];
-        const int d = scan_row(lane, nd);
-        st_need[lane] = nd;
-        st_key[lane] = (st_key[lane] << 8) | (uint32_t)d;
+    for (int e = 0; e < 4; ++e) pre[e] = st_key[4 * g + e];
+    const int hi_shift = 32 - 8 * level, lo_shift = 24 - 8 * level;
+    zero_hist();
+    sweep([&](int e, int, int, int, bool valid, float s) {
+      if (valid && bin_of(s, inv_w[e]) == b1[e]) {
+        const uint32_t key = score_key(s);
+        if (level == 0 || (key >> hi_shift) == pre[e])
+          atomicAdd(&sh[(4 * g + e) * kHStride + ((key >> lo_shift) & 255u)], 1u);
       }
-      __syncthreads();
+    });
+    __syncthreads();
+    if (tid < 16 && st_mode[tid] == kOverflow) {
+      int cum = 0, d = 0, nd = st_need[tid];
+      for (int bin = 255; bin >= 0; --bin) {
+        const int c = (int)sh[tid * kHStride + bin];
+        if (cum + c >= nd) { d = bin; break; }
+        cum += c;
+      }
+      st_need[tid] = nd - cum;
+      st_key[tid] = (st_key[tid] << 8) | (uint32_t)d;
     }
-    if (lane < 16 && st_mode[lane] == kOverflow) st_mode[lane] = kResolved;
     __syncthreads();
   }
+  // wave 0 marks the winners of the overflow rows in key order (tie ranks need order)
+  if (wave == 0) {
+    uint32_t theta[4];
+    int tie_need[4], tie_seen[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      theta[e] = st_key[4 * g + e];
+      tie_need[e] = st_need[4 * g + e];
+      tie_seen[e] = 0;
+    }
+    const uint64_t gmask = 0xffffull << (16 * g);
+    rgp.load_keys(0, p.T, lane, kn);
+    for (int t = 0; t < ntl; ++t) {
+#pragma unroll
+      for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = kn[s];
+      if (t + 1 < ntl) rgp.load_keys((t + 1) * 16, p.T, lane, kn);
+      floatx4 acc[kHi];
+      rgp.mma(kb, acc);
+      const int col = t * 16 + lr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = r0 + 4 * g + e;
+        const bool valid = mode[e] == kActive && col <= row;
+        const float s = valid ? rgp.score(acc, e) : 0.f;
+        const bool inbin = valid && bin_of(s, inv_w[e]) == b1[e];
+        const uint32_t key = score_key(s);
+        const bool tie = inbin && key == theta[e];
+        const uint64_t tmask = ballot64(tie) & gmask;
+        const int trank = tie_seen[e] + count_below(tmask);
+        tie_seen[e] += __popcll(tmask);
+        if (inbin && (key > theta[e] || (tie && trank < tie_need[e])))
+          atomicOr(&bbase[(int64_t)row * b_st + (col >> 5)], 1u << (col & 31));
+      }
+    }
+  }
+}
 
-  // ---- pass 3: ordered emission ------------------------------------------
-  int tie_need[4], tie_seen[4], emitted[4];
+// ---------------------------------------------------------------------------
+// Bitmask -> ascending indices + count, one 256-thread block per row.  The
+// tail of a row with fewer than k selected keys is t+1, t+2, ... (the
+// lowest-index invalid entries, as the selector orders them).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bits_to_indices_kernel(const uint32_t* __restrict__ bits, int64_t b_sb,
+                                                              int64_t b_st, int T, int W, int k_eff,
+                                                              int32_t* __restrict__ idx_out,
+                                                              int32_t* __restrict__ count_out) {
+  __shared__ int wave_tot[4];
+  const int row = blockIdx.x;
+  const int b = row / T, t = row % T;
+  const uint32_t* brow = bits + b * b_sb + (int64_t)t * b_st;
+  int32_t* orow = idx_out + (int64_t)row * k_eff;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (W + 255) / 256;       // contiguous words per thread
+  const int w0 = min(W, tid * per), w1 = min(W, w0 + per);
+  int cnt = 0;
+  for (int wd = w0; wd < w1; ++wd) cnt += __popc(brow[wd]);
+  // exclusive prefix over the block
+  int incl = cnt;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    mode[e] = st_mode[4 * g + e];
-    theta[e] = st_key[4 * g + e];
-    tie_need[e] = st_need[4 * g + e];
-    tie_seen[e] = 0;
-    emitted[e] = 0;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
   }
-  const uint64_t gmask = 0xffffull << (16 * g);
-  sweep([&](int e, int row, int col, bool valid, float s) {
-    const uint32_t key = score_key(s);
-    const bool tie = valid && key == theta[e];
-    const uint64_t tmask = ballot64(tie) & gmask;
-    const int trank = tie_seen[e] + count_below(tmask);
-    tie_seen[e] += __popcll(tmask);
-    const bool sel = valid && (key > theta[e] || (tie && trank < tie_need[e]));
-    const uint64_t smask = ballot64(sel) & gmask;
-    const int pos = emitted[e] + count_below(smask);
-    if (sel && pos < k_eff) idx_out[(out_row0 + row) * k_eff + pos] = col;
-    emitted[e] += __popcll(smask);
-  });
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int base = incl - cnt, total = 0;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int row = r0 + 4 * g + e;
-    if (mode[e] != kTrivial && lr == 0) count_out[out_row0 + row] = emitted[e];
+  for (int w = 0; w < 4; ++w) {
+    if (w < wave) base += wave_tot[w];
+    total += wave_tot[w];
   }
+  int pos = base;
+  for (int wd = w0; wd < w1; ++wd) {
+    uint32_t m = brow[wd];
+    while (m) {
+      const int bit = __ffs(m) - 1;
+      m &= m - 1;
+      if (pos < k_eff) orow[pos] = wd * 32 + bit;
+      ++pos;
+    }
+  }
+  const int n = min(total, k_eff);
+  for (int i = n + tid; i < k_eff; i += 256) orow[i] = t + 1 + (i - n);
+  if (tid == 0) count_out[row] = n;
 }
 
 }  // namespace gsa
@@ -472,20 +562,31 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                                   const void* w, int64_t w_sb, int64_t w_st,
                                   const float* bias, float scale,
                                   int B, int T, int Hi, int di, int k_eff, int dtype,
+                                  uint32_t* bits, int64_t b_sb, int64_t b_st,
                                   int32_t* idx_out, int32_t* count_out,
                                   void* stream) {
   int st = check_indexer_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype);
   if (st) return st;
-  if (!idx_out || !count_out) return GSA_ERR_NULL;
+  if (!bits) return GSA_ERR_NULL;
+  if ((idx_out == nullptr) != (count_out == nullptr)) return GSA_ERR_NULL;
   if (k_eff < 1 || k_eff > T) return GSA_ERR_K;
-  if (!aligned(idx_out, 4) || !aligned(count_out, 4)) return GSA_ERR_ALIGN;
+  const int W = 2 * ((T + 63) / 64);
+  if (b_st < W || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
+  if (!aligned(bits, 8) || (b_st % 2) || (b_sb % 2)) return GSA_ERR_ALIGN;
+  if (idx_out && (!aligned(idx_out, 4) || !aligned(count_out, 4))) return GSA_ERR_ALIGN;
+  if ((int64_t)B * T > 0x7fffffffLL) return GSA_ERR_SHAPE;
   gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
   const int ngroups = (T + 15) / 16;
-  dim3 grid(B * ngroups), block(64);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == GSA_DTYPE_BF16)
-    hipLaunchKernelGGL(gsa::indexer_select_kernel<uint16_t>, grid, block, 0, s, a, k_eff, idx_out, count_out);
+    hipLaunchKernelGGL(gsa::indexer_bits_kernel<uint16_t>, dim3(B * ngroups), dim3(256), 0, s, a, k_eff, bits,
+                       b_sb, b_st);
   else
-    hipLaunchKernelGGL(gsa::indexer_select_kernel<float>, grid, block, 0, s, a, k_eff, idx_out, count_out);
+    hipLaunchKernelGGL(gsa::indexer_bits_kernel<float>, dim3(B * ngroups), dim3(256), 0, s, a, k_eff, bits,
+                       b_sb, b_st);
+  st = launch_status();
+  if (st || !idx_out) return st;
+  hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_eff,
+                     idx_out, count_out);
   return launch_status();
 }

@@ -355,11 +355,16 @@ class GatedSparseAttention(nn.Module):
         v["_buf"] = comb
         return v
 
-    def select(self, views, T: int):
-        """Fused indexer + top-k on the current stream -> (idx int32, count int32)."""
+    def select(self, views, T: int, indices: bool = True):
+        """Fused indexer + top-k on the current stream -> (bits, idx, count).
+
+        bits: the selection bitmask int32 [B,T,2*ceil(T/64)]; idx/count
+        (ascending int32, per-row count) only when ``indices``.
+        """
         k_eff = self.topk_selector.k_effective(T)
         bias = self.indexer.idx_bias.detach().float().contiguous()
-        return _abi.indexer_select(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale, k_eff)
+        return _abi.indexer_select(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale, k_eff,
+                                   indices=indices)
 
     def uses_dense(self, dtype: torch.dtype) -> bool:
         if self.attn_impl not in ("auto", "dense", "gather"):
@@ -395,8 +400,7 @@ class GatedSparseAttention(nn.Module):
         side.wait_stream(cur)
         with torch.cuda.stream(side):
             _range_push("gsa_hip/indexer_select")
-            idx, cnt = self.select(views, T)
-            bits = _abi.selection_mask(idx, T, count=cnt) if dense else None
+            bits, idx, cnt = self.select(views, T, indices=not dense)
             _range_pop()
 
         # Track B: RoPE(k) and the value gate on the current stream

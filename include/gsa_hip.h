@@ -102,10 +102,13 @@ int gsa_topk_select(const float* scores, int64_t s_sb, int64_t s_st,
  * Indexer and selector fused: the [B,T,T] score matrix is never stored.
  * Replaces the indexer track of the optimized forward (gsa_triton/gsa_opt.py:
  * 663-677: fused_gated_indexer + AdaptiveTopKSelector + ascending sort).
- * Produces exactly what gsa_indexer_scores followed by gsa_topk_select
- * (GSA_ORDER_INDEX_ASC, causal) produce: idx_out int32 [B,T,k_eff] holds row
- * t's min(t+1, k_eff) selected keys ascending, followed by t+1, t+2, ... for
- * rows with fewer than k_eff causal keys; count_out int32 [B,T].
+ * Selects exactly what gsa_indexer_scores followed by gsa_topk_select
+ * (causal) select.  Always writes the selection as a bitmask: bits uint32
+ * [B,T,W] (strides b_sb, b_st; W = 2*ceil(T/64) words per row; bit j of row
+ * t set iff key j is selected; 8-byte aligned rows), the form gsa_dense_attn
+ * takes.  When idx_out and count_out are given it also writes, like
+ * GSA_ORDER_INDEX_ASC: idx_out int32 [B,T,k_eff] = row t's min(t+1, k_eff)
+ * selected keys ascending, followed by t+1, t+2, ...; count_out int32 [B,T].
  * Supported: Hi == 4, di == 64, 1 <= k_eff <= T.
  */
 int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
@@ -113,6 +116,7 @@ int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                        const void* w, int64_t w_sb, int64_t w_st,
                        const float* bias, float scale,
                        int B, int T, int Hi, int di, int k_eff, int dtype,
+                       uint32_t* bits, int64_t b_sb, int64_t b_st,
                        int32_t* idx_out, int32_t* count_out,
                        void* stream);
 

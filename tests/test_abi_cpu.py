@@ -78,20 +78,51 @@ def test_indexer_scores_validation(lib):
 
 def _select(lib, **kw):
     a = dict(q=P, qsb=0, qst=256, k=P, ksb=0, kst=64, w=P, wsb=0, wst=4, bias=P, scale=0.125,
-             B=1, T=32, Hi=4, di=64, k_eff=8, dtype=1, idx=P, cnt=P)
+             B=1, T=32, Hi=4, di=64, k_eff=8, dtype=1, bits=P, bsb=0, bst=2, idx=P, cnt=P)
     a.update(kw)
     return lib.gsa_indexer_select(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["w"], a["wsb"],
                                   a["wst"], a["bias"], a["scale"], a["B"], a["T"], a["Hi"], a["di"],
-                                  a["k_eff"], a["dtype"], a["idx"], a["cnt"], None)
+                                  a["k_eff"], a["dtype"], a["bits"], a["bsb"], a["bst"], a["idx"], a["cnt"], None)
 
 
 def test_indexer_select_validation(lib):
     assert _select(lib, bias=None) == 1
-    assert _select(lib, cnt=None) == 1
+    assert _select(lib, bits=None) == 1
+    assert _select(lib, cnt=None) == 1            # idx without count
     assert _select(lib, k_eff=0) == 5
     assert _select(lib, k_eff=33) == 5
     assert _select(lib, dtype=-1) == 3
     assert _select(lib, k=MIS) == 4
+    assert _select(lib, bst=1) == 2               # fewer words than 2*ceil(T/64)
+    assert _select(lib, bits=P + 4) == 4          # rows must be 8-byte aligned
+
+
+def test_dense_path_validation(lib):
+    f = lib.gsa_selection_mask
+    assert f(None, 0, 8, 8, None, None, 1, 4, 4, P, 0, 2, None) == 1
+    assert f(P, 0, 8, 8, None, None, 1, 4, 4, P + 4, 0, 2, None) == 4
+    assert f(P, 0, 8, 8, None, None, 1, 4, 1 << 20, P, 0, 2, None) == 2     # mask row too long for LDS
+    g = lib.gsa_dense_attn
+    ok = dict(q=P, qsb=0, qst=2048, k=P, ksb=0, kst=2048, vt=P, vtsb=0, vtsh=8192, ldv=64, bits=P, bsb=0, bst=2,
+              og=P, osb=0, ost=2048, cos=P, sin=P, cst=128, out=P, outsb=0, outst=2048,
+              B=1, T=4, Tkv=4, H=16, d=128, scale=0.088, dtype=1, flags=3, causal=1)
+
+    def call(**kw):
+        a = dict(ok)
+        a.update(kw)
+        return g(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["vt"], a["vtsb"], a["vtsh"], a["ldv"],
+                 a["bits"], a["bsb"], a["bst"], a["og"], a["osb"], a["ost"], a["cos"], a["sin"], a["cst"],
+                 a["out"], a["outsb"], a["outst"], a["B"], a["T"], a["Tkv"], a["H"], a["d"], a["scale"],
+                 a["dtype"], a["flags"], a["causal"], None)
+
+    assert call(bits=None) == 1
+    assert call(dtype=0) == 3                     # bf16 only
+    assert call(ldv=32) == 2                      # rows shorter than ceil(Tkv/64)*64
+    assert call(flags=4) == 6
+    assert call(bst=3) == 4
+    p = lib.gsa_prologue_vt
+    assert p(P, 0, 2048, P, 0, 2048, P, 0, 2048, P, P, 128, 1, 4, 16, 128, 1, P, P, 100, None) == 2   # ldv % 64
+    assert p(P, 0, 2048, None, 0, 2048, P, 0, 2048, P, P, 128, 1, 4, 16, 128, 1, P, P, 64, None) == 1
 
 
 def test_topk_validation(lib):

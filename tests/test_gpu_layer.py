@@ -45,7 +45,7 @@ def _gpu_selection(model, x_dev):
     """(ascending idx, count) the layer's fused indexer+select produces for x."""
     with torch.no_grad():
         views = model.project(x_dev)
-        idx, cnt = model.select(views, x_dev.shape[1])
+        _, idx, cnt = model.select(views, x_dev.shape[1])
     return idx.cpu(), cnt.cpu()
 
 
