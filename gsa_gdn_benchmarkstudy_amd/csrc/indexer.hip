@@ -245,16 +245,26 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
   __syncthreads();
   if (tid < 16 && st_mode[tid] == kActive) st_any[0] = 1;
 
-  // Chunks of tile rg_idx+1 .. end of the 64-key tile are zero for every row;
-  // trivial rows get their causal prefix now.
+  // Every chunk after the diagonal tile is zero; trivial rows get their
+  // causal prefix now.  (The zeroing is largest for the lightest groups.)
   const int ntl = rg_idx + 1;                  // causal 16-key tiles 0 .. rg_idx
-  const int zend = (rg_idx | 3) + 1;
+  const int zend = (rg_idx | 3) + 1;           // chunks up to the end of the 64-key tile
   for (int i = tid; i < 16 * zend; i += 256) {
     const int rl = i / zend, tile = i % zend;
     const int row = r0 + rl;
     if (row >= p.T) continue;
     if (tile >= ntl) b16[row * row16 + tile] = 0;
     else if (st_mode[rl] == kTrivial) b16[row * row16 + tile] = prefix_chunk(row, tile);
+  }
+  {
+    const int W = 2 * ((p.T + 63) >> 6);
+    const int d0 = zend >> 2;                    // first 8-byte pair of words past the 64-key tile
+    const int npair = (W >> 1) - d0;
+    for (int i = tid; i < 16 * npair; i += 256) {
+      const int rl = i / npair, pr = d0 + i % npair;
+      const int row = r0 + rl;
+      if (row < p.T) reinterpret_cast<uint2*>(bbase + (int64_t)row * b_st)[pr] = uint2{0u, 0u};
+    }
   }
   __syncthreads();
   if (!st_any[0]) return;
