@@ -229,8 +229,10 @@ def main():
                    "traffic": profiled_traffic("gsa_sparse_attn", args.config),
                    "algorithmic_bytes": abytes, "valid_pairs": P, "ms": gather_ms}
     if attn_impl == "dense":
-        nqb = (T + 63) // 64
-        dense_flops = 4 * B * H * DH * 64 * 64 * sum(min(qb * 64 + 63, T - 1) // 64 + 1 for qb in range(nqb))
+        qrows = 128                              # query rows per block of gsa_dense_attn
+        nqb = (T + qrows - 1) // qrows
+        dense_flops = 4 * B * H * DH * qrows * 64 * sum(min(qb * qrows + qrows - 1, T - 1) // 64 + 1
+                                                         for qb in range(nqb))
         ach = aflops / (attn_ms * 1e-3) / 1e12
         roofline = {"kernel": "gsa_dense_attn", "bound": "mfma", "achieved": ach, "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": ach / BF16_PEAK_TFLOPS,

@@ -1,5 +1,5 @@
 // Block-dense sparse attention on gfx950 MFMA: every causal key tile is
-// streamed once per 64-row query block and the exact top-k selection is
+// streamed once per 128-row query block and the exact top-k selection is
 // applied as a bitmask, so masked-out keys get probability 0.  Same function
 // as the gather kernel (softmax over each row's selected keys), different
 // work: dense MFMA over the causal triangle instead of per-row gathers.
@@ -9,19 +9,20 @@
 // selection bits [B,T,W] uint32, W = 2*ceil(Tkv/64): bit j of row t set iff
 // key j is selected and valid for query t.
 //
-// Per block: one head, 64 query rows, 4 waves of 16 rows.  With
-// v_mfma_f32_16x16x32_bf16 both products are computed transposed,
+// Per block: one head, 128 query rows, 4 waves of 32 rows, 64-key tiles
+// staged in LDS.  With v_mfma_f32_32x32x16_bf16 both products are computed
+// transposed,
 //   S^T = K Q^T    (A = K tile from LDS, B = this wave's q, in registers)
 //   O^T = V^T P^T  (A = V^T tile from LDS, B = P in registers)
-// so in both outputs lane l holds column l%16 = one query row: the softmax
-// state of a query lives in the lanes of its column and P never moves
-// between lanes.  Lane group g = l/16 holds keys 16c+4g+e (c = 0..3 subtiles,
-// e = 0..3) of S^T and d = 16n+4g+e (n = 0..7) of O^T.
+// so in both outputs lane l holds column l%32 = one query row: a query's
+// softmax state lives in its two lanes (l and l^32) and P never moves between
+// lanes.  Accumulator r of lane l is row 8*(r/4) + 4*(l/32) + r%4 of the
+// 32x32 block: keys of S^T, head dims of O^T.
 #include "gsa_common.h"
 
 namespace gsa {
 
-constexpr int kDQ = 64;          // query rows per block
+constexpr int kDQ = 128;         // query rows per block (32 per wave)
 constexpr int kDK = 64;          // keys per tile
 constexpr int kKS = 128 + 8;     // LDS row stride of the K tile (elements): conflict-free 16-B reads
 constexpr int kVS = kDK + 12;    // LDS row stride of the V^T tile (elements): conflict-free 8-B reads
@@ -133,66 +134,73 @@ struct DenseArgs {
 
 constexpr int kDenseCausal = 1 << 8;   // internal flag: skip key tiles after the block's last row
 
-__device__ __forceinline__ float xor16(float v) { return __shfl_xor(v, 16, 64); }
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+// Two fp32 -> packed bf16 (round to nearest even, hardware convert).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs p) {
   __shared__ __align__(16) uint16_t sK[kDK * kKS];
   __shared__ __align__(16) uint16_t sVt[128 * kVS];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = lane >> 4, lr = lane & 15;
+  const int i32 = lane & 31, h = lane >> 5;
   // heaviest query blocks first
   const int nbh = p.B * p.H;
   const int qb = p.nqb - 1 - (int)(blockIdx.x / nbh);
   const int rem = blockIdx.x % nbh;
-  const int b = rem / p.H, h = rem % p.H;
+  const int b = rem / p.H, hd = rem % p.H;
   const int q0 = qb * kDQ;
-  const int qrow = q0 + 16 * w + lr;
+  const int qrow = q0 + 32 * w + i32;
   const int qr = min(qrow, p.T - 1);
 
-  // ---- q: B operand of S^T, lane supplies d = 32s + 8g .. +7 of its row ----
-  u32x4 qraw[4];
-  const uint16_t* qp = p.q + b * p.q_sb + (int64_t)qr * p.q_st + h * 128;
+  // ---- q: B operand of S^T; lane supplies d = 16s + 8h .. +7 of its row ----
+  u32x4 qraw[8];
+  const uint16_t* qp = p.q + b * p.q_sb + (int64_t)qr * p.q_st + hd * 128;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) qraw[s] = *reinterpret_cast<const u32x4*>(qp + 32 * s + 8 * g);
+  for (int s = 0; s < 8; ++s) qraw[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * h);
   if (p.flags & GSA_ATTN_ROPE_Q) {
-    // rotate_half partner of d (d < 64: -x[d+64]; else x[d-64]) is register s^2
-    float x[4][8], y[4][8];
+    // rotate_half partner of d (d < 64: -x[d+64]; else x[d-64]) is register s^4
+    float x[8][8];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { x[s][2 * i] = bf16lo(qraw[s][i]); x[s][2 * i + 1] = bf16hi(qraw[s][i]); }
+      for (int j = 0; j < 4; ++j) { x[s][2 * j] = bf16lo(qraw[s][j]); x[s][2 * j + 1] = bf16hi(qraw[s][j]); }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float c[8], sn[8];
-      load8(p.cos + (int64_t)qr * p.cs_st + 32 * s + 8 * g, c);
-      load8(p.sin + (int64_t)qr * p.cs_st + 32 * s + 8 * g, sn);
+    for (int s = 0; s < 8; ++s) {
+      float c[8], sn[8], y[8];
+      load8(p.cos + (int64_t)qr * p.cs_st + 16 * s + 8 * h, c);
+      load8(p.sin + (int64_t)qr * p.cs_st + 16 * s + 8 * h, sn);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float a = round_bf16(x[s][i] * c[i]);
-        const float r = round_bf16((s < 2 ? -x[s + 2][i] : x[s - 2][i]) * sn[i]);
-        y[s][i] = round_bf16(a + r);
+      for (int j = 0; j < 8; ++j) {
+        const float a = round_bf16(x[s][j] * c[j]);
+        const float r = round_bf16((s < 4 ? -x[s + 4][j] : x[s - 4][j]) * sn[j]);
+        y[j] = round_bf16(a + r);
       }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qraw[s][j] = pack_bf16(y[2 * j], y[2 * j + 1]);
     }
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qraw[s][i] = pack_bf16(y[s][2 * i], y[s][2 * i + 1]);
   }
-  bf16x8 qop[4];
+  bf16x8 qop[8];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) qop[s] = __builtin_bit_cast(bf16x8, qraw[s]);
+  for (int s = 0; s < 8; ++s) qop[s] = __builtin_bit_cast(bf16x8, qraw[s]);
 
-  floatx4 o[8];
+  floatx16 o[4];
 #pragma unroll
-  for (int n = 0; n < 8; ++n) o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
   float m = -__builtin_inff(), l = 0.f;
 
   const int last_key = (p.flags & kDenseCausal) ? min(p.Tkv - 1, q0 + kDQ - 1) : p.Tkv - 1;
   const int nkt = last_key / kDK + 1;
-  const uint16_t* kbase = p.k + b * p.k_sb + h * 128;
-  const uint16_t* vtb = p.vt + b * p.vt_sb + h * p.vt_sh;
+  const uint16_t* kbase = p.k + b * p.k_sb + hd * 128;
+  const uint16_t* vtb = p.vt + b * p.vt_sb + hd * p.vt_sh;
   const uint32_t* brow = p.bits + b * p.b_sb + (int64_t)qr * p.b_st;
 
   // staging: K tile = 64 keys x 16 chunks of 16 B, V^T tile = 128 rows x 8 chunks
@@ -238,95 +246,98 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs p) {
     __syncthreads();
     if (kt + 1 < nkt) fetch(kt + 1);   // next tile's loads fly during this tile's math
 
-    const uint64_t mbits = qrow < p.T ? *reinterpret_cast<const uint64_t*>(brow + 2 * kt) : 0ull;
+    // selection bits of this lane's keys, pre-shifted by its lane half
+    const uint64_t mb = (qrow < p.T ? *reinterpret_cast<const uint64_t*>(brow + 2 * kt) : 0ull) >> (4 * h);
 
-    // ---- S^T = K Q^T ----
-    floatx4 sacc[4];
+    // ---- S^T = K Q^T: two 32-key subtiles ----
+    floatx16 sacc[2];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 2; ++c) {
+      floatx16 acc;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(sK + (16 * c + lr) * kKS + 32 * s + 8 * g);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[s], acc, 0, 0, 0);
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(sK + (32 * c + i32) * kKS + 16 * s + 8 * h);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qop[s], acc, 0, 0, 0);
       }
       sacc[c] = acc;
     }
 
     // ---- masked online softmax (log2 domain) ----
-    float sv[4][4];
     float mx = -__builtin_inff();
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool sel = (mbits >> (16 * c + 4 * g + e)) & 1ull;
-        sv[c][e] = sel ? sacc[c][e] * p.scale_l2 : -__builtin_inff();
-        mx = fmaxf(mx, sv[c][e]);
+      for (int r = 0; r < 16; ++r) {
+        const bool sel = (mb >> (32 * c + 8 * (r >> 2) + (r & 3))) & 1ull;
+        sacc[c][r] = sel ? sacc[c][r] * p.scale_l2 : -__builtin_inff();
+        mx = fmaxf(mx, sacc[c][r]);
       }
-    mx = fmaxf(mx, xor16(mx));
     mx = fmaxf(mx, xor32(mx));
     const float mnew = fmaxf(m, mx);
-    const float alpha = mnew == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m - mnew);
-    uint32_t pk[2][4];
+    const float msafe = mnew == -__builtin_inff() ? 0.f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(m - msafe);
+    // P as the B operand of O^T: k-step ks = 2c + s2 covers keys
+    // 32c + 16*s2 + 4h + {0..3} and 32c + 16*s2 + 8 + 4h + {0..3}
+    uint32_t pk[4][4];
     float lsum = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int half = 0; half < 2; ++half)
-#pragma unroll
-        for (int e2 = 0; e2 < 2; ++e2) {
-          const int c = 2 * kk + half;
-          const float p0 = sv[c][2 * e2] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(sv[c][2 * e2] - mnew);
-          const float p1 = sv[c][2 * e2 + 1] == -__builtin_inff() ? 0.f
-                                                                   : __builtin_amdgcn_exp2f(sv[c][2 * e2 + 1] - mnew);
-          const uint32_t bits2 = pack_bf16(p0, p1);
-          pk[kk][2 * half + e2] = bits2;
-          lsum += bf16lo(bits2) + bf16hi(bits2);   // normalise with the rounded weights
-        }
+      for (int r = 0; r < 16; r += 2) {
+        const uint32_t v2 = cvt_pk_bf16(__builtin_amdgcn_exp2f(sacc[c][r] - msafe),
+                                        __builtin_amdgcn_exp2f(sacc[c][r + 1] - msafe));
+        pk[2 * c + (r >> 3)][(r & 7) >> 1] = v2;
+        lsum += bf16lo(v2) + bf16hi(v2);   // normalise with the rounded weights
+      }
     l = l * alpha + lsum;
+    if (ballot64(alpha != 1.f)) {          // skip the rescale when no row max moved
 #pragma unroll
-    for (int n = 0; n < 8; ++n)
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[n][e] *= alpha;
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    }
     m = mnew;
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pk[kk][0], pk[kk][1], pk[kk][2], pk[kk][3]});
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pk[ks][0], pk[ks][1], pk[ks][2], pk[ks][3]});
+      const int koff = 32 * (ks >> 1) + 16 * (ks & 1) + 4 * h;
 #pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const uint16_t* vr = sVt + (16 * n + lr) * kVS + 32 * kk + 4 * g;
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint16_t* vr = sVt + (32 * dt + i32) * kVS + koff;
         const uint2 a0 = *reinterpret_cast<const uint2*>(vr);
-        const uint2 a1 = *reinterpret_cast<const uint2*>(vr + 16);
+        const uint2 a1 = *reinterpret_cast<const uint2*>(vr + 8);
         const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{a0.x, a0.y, a1.x, a1.y});
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[n], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[dt], 0, 0, 0);
       }
     }
   }
 
   // ---- epilogue: normalise, bf16, optional output gate ----
-  l += xor16(l);
   l += xor32(l);
   if (qrow < p.T) {
-    uint16_t* op = p.out + b * p.out_sb + (int64_t)qrow * p.out_st + h * 128;
-    const uint16_t* gp = (p.flags & GSA_ATTN_OUT_GATE) ? p.og + b * p.o_sb + (int64_t)qrow * p.o_st + h * 128
+    uint16_t* op = p.out + b * p.out_sb + (int64_t)qrow * p.out_st + hd * 128;
+    const uint16_t* gp = (p.flags & GSA_ATTN_OUT_GATE) ? p.og + b * p.o_sb + (int64_t)qrow * p.o_st + hd * 128
                                                        : nullptr;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      const int d0 = 16 * n + 4 * g;
-      float r[4];
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = round_bf16(l > 0.f ? o[n][e] / l : 0.f);
-      if (gp) {
-        const uint2 gw = *reinterpret_cast<const uint2*>(gp + d0);
-        const float gl[4] = {bf16lo(gw.x), bf16hi(gw.x), bf16lo(gw.y), bf16hi(gw.y)};
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d0 = 32 * dt + 8 * r4 + 4 * h;
+        float r[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = round_bf16(r[e] * round_bf16(sigmoidf_fast(gl[e])));
+        for (int e = 0; e < 4; ++e) r[e] = round_bf16(l > 0.f ? o[dt][4 * r4 + e] / l : 0.f);
+        if (gp) {
+          const uint2 gw = *reinterpret_cast<const uint2*>(gp + d0);
+          const float gl[4] = {bf16lo(gw.x), bf16hi(gw.x), bf16lo(gw.y), bf16hi(gw.y)};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r[e] = round_bf16(r[e] * round_bf16(sigmoidf_fast(gl[e])));
+        }
+        *reinterpret_cast<uint2*>(op + d0) = uint2{pack_bf16(r[0], r[1]), pack_bf16(r[2], r[3])};
       }
-      *reinterpret_cast<uint2*>(op + d0) = uint2{pack_bf16(r[0], r[1]), pack_bf16(r[2], r[3])};
-    }
   }
 }
 
@@ -398,7 +409,7 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   if (B < 1 || T < 1 || Tkv < 1 || d != 128 || H < 1 || H > 64) return GSA_ERR_SHAPE;
   const int nkt = (Tkv + 63) / 64;
   if (ldv < nkt * 64 || ldv % 64 != 0) return GSA_ERR_SHAPE;
-  const int nqb = (T + 63) / 64;
+  const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
   if ((int64_t)B * H * nqb > 0x7fffffffLL) return GSA_ERR_SHAPE;
   if (!vec_ok(q, q_sb, q_st, dtype) || !vec_ok(k, k_sb, k_st, dtype) || !vec_ok(vt, vt_sb, vt_sh, dtype) ||
       !vec_ok(out, out_sb, out_st, dtype) || !aligned(bits, 8) || (b_sb % 2) || (b_st % 2))
