@@ -133,6 +133,7 @@ struct DenseArgs {
 };
 
 constexpr int kDenseCausal = 1 << 8;   // internal flag: skip key tiles after the block's last row
+constexpr float kLazy = 8.f;           // log2 headroom of the lazy softmax reference
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -144,7 +145,7 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-__global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs p) {
+__global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
   __shared__ __align__(16) uint16_t sK[kDK * kKS];
   __shared__ __align__(16) uint16_t sVt[128 * kVS];
 
@@ -264,20 +265,24 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs p) {
       sacc[c] = acc;
     }
 
-    // ---- masked online softmax (log2 domain) ----
+    // ---- masked online softmax (log2 domain, lazy reference max) ----
+    // p = 2^(s*scale*log2e - m) against a per-row reference m that only moves
+    // when the row max exceeds it by more than kLazy: p <= 2^kLazy, so O and l
+    // are rescaled rarely; out = O / l does not depend on m.
     float mx = -__builtin_inff();
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const bool sel = (mb >> (32 * c + 8 * (r >> 2) + (r & 3))) & 1ull;
-        sacc[c][r] = sel ? sacc[c][r] * p.scale_l2 : -__builtin_inff();
+        sacc[c][r] = sel ? sacc[c][r] : -__builtin_inff();
         mx = fmaxf(mx, sacc[c][r]);
       }
-    mx = fmaxf(mx, xor32(mx));
-    const float mnew = fmaxf(m, mx);
-    const float msafe = mnew == -__builtin_inff() ? 0.f : mnew;
-    const float alpha = __builtin_amdgcn_exp2f(m - msafe);
+    mx = fmaxf(mx, xor32(mx)) * p.scale_l2;
+    const bool bump = mx > m + kLazy || (m == -__builtin_inff() && mx != -__builtin_inff());
+    const float mref = bump ? mx : m;
+    const float alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
+    const float msafe = mref == -__builtin_inff() ? 0.f : mref;
     // P as the B operand of O^T: k-step ks = 2c + s2 covers keys
     // 32c + 16*s2 + 4h + {0..3} and 32c + 16*s2 + 8 + 4h + {0..3}
     uint32_t pk[4][4];
@@ -286,19 +291,19 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs p) {
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const uint32_t v2 = cvt_pk_bf16(__builtin_amdgcn_exp2f(sacc[c][r] - msafe),
-                                        __builtin_amdgcn_exp2f(sacc[c][r + 1] - msafe));
-        pk[2 * c + (r >> 3)][(r & 7) >> 1] = v2;
-        lsum += bf16lo(v2) + bf16hi(v2);   // normalise with the rounded weights
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[c][r], p.scale_l2, -msafe));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[c][r + 1], p.scale_l2, -msafe));
+        pk[2 * c + (r >> 3)][(r & 7) >> 1] = cvt_pk_bf16(p0, p1);
+        lsum += p0 + p1;
       }
     l = l * alpha + lsum;
-    if (ballot64(alpha != 1.f)) {          // skip the rescale when no row max moved
+    if (ballot64(bump)) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     }
-    m = mnew;
+    m = mref;
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
