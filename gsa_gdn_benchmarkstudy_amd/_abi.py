@@ -33,7 +33,7 @@ ATTN_OUT_GATE = 2
 EXPORTS = (
     "gsa_abi_version", "gsa_status_string", "gsa_indexer_scores", "gsa_topk_select",
     "gsa_indexer_select", "gsa_prologue", "gsa_sparse_attn", "gsa_prologue_vt",
-    "gsa_selection_mask", "gsa_dense_attn",
+    "gsa_selection_mask", "gsa_dense_attn", "gsa_dense_attn_workspace_bytes",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -56,7 +56,8 @@ _PROTOS = {
     "gsa_selection_mask": ([_vp, _i64, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp], _i32),
     "gsa_dense_attn": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i32, _vp, _i64, _i64,
                         _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64,
-                        _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp], _i32),
+                        _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
+    "gsa_dense_attn_workspace_bytes": ([_i32, _i32, _i32], ctypes.c_size_t),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -353,8 +354,10 @@ def selection_mask(idx, Tkv: int, count=None, mask=None, out=None):
 
 
 def dense_attn(q, k, vt, bits, scale: float, og=None, cos=None, sin=None, flags: int = 0,
-               causal: bool = True, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Block-dense masked attention -> out [B,T,H,d] (bf16)."""
+               causal: bool = True, out: Optional[torch.Tensor] = None,
+               ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block-dense masked attention -> out [B,T,H,d] (bf16).  ``ws``: optional
+    workspace (uint8 device tensor of at least dense_attn_workspace_bytes)."""
     lib = load()
     _need_cuda(q, k, vt, bits, og, cos, sin)
     B, T, H, d = q.shape
@@ -375,12 +378,16 @@ def dense_attn(q, k, vt, bits, scale: float, og=None, cos=None, sin=None, flags:
     if out is None:
         out = torch.empty(B, T, H, d, device=q.device, dtype=q.dtype)
     _expect(tuple(out.shape) == (B, T, H, d) and out.dtype == q.dtype, "out: [B,T,H,d] in q's dtype")
+    nbytes = lib.gsa_dense_attn_workspace_bytes(B, T, Tkv)
+    if ws is None:
+        ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    _expect(ws.numel() * ws.element_size() >= nbytes and ws.is_contiguous(), "workspace too small")
     os_ = _rows(og, HD) if og is not None else (0, 0)
     cs = cos.stride(0) if cos is not None else 0
     st = lib.gsa_dense_attn(_ptr(q), *_rows(q, HD), _ptr(k), *_rows(k, HD), _ptr(vt), vt.stride(0),
                             vt.stride(1), vt.shape[3], _ptr(bits), bits.stride(0), bits.stride(1),
                             _ptr(og), *os_, _ptr(cos), _ptr(sin), cs, _ptr(out), *_rows(out, HD),
                             B, T, Tkv, H, d, float(scale), dtype_code(q.dtype), int(flags), int(bool(causal)),
-                            _stream(q))
+                            _ptr(ws), nbytes, _stream(q))
     _check(st, "gsa_dense_attn")
     return out

@@ -117,13 +117,42 @@ __global__ __launch_bounds__(256) void selection_mask_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Selection bitmask -> per-lane masks of the dense kernel's score slots.
+// For 32-row group g (rows 32g + i), 64-key tile kt and score slot
+// s = 16c + r (c = 0,1; r = 0..15), lm[b][g][kt][s] bit (32h + i) is the
+// selection bit of row 32g+i and key 64kt + 32c + 8*(r/4) + 4h + r%4 -- the
+// key that accumulator r of lane (h, i) holds in the S^T MFMA output.  One
+// wave per (b, g, kt).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restrict__ bits, int64_t b_sb,
+                                                        int64_t b_st, int T, int G, int NT, int nwaves,
+                                                        uint64_t* __restrict__ lm) {
+  const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wv >= nwaves) return;
+  const int kt = wv % NT, bg = wv / NT;
+  const int g = bg % G, b = bg / G;
+  const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+  const int row = 32 * g + i;
+  uint64_t word = row < T ? *reinterpret_cast<const uint64_t*>(bits + b * b_sb + (int64_t)row * b_st + 2 * kt) : 0ull;
+  word >>= 4 * h;
+  uint64_t* out = lm + ((int64_t)bg * NT + kt) * 32;
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const uint64_t m = ballot64((word >> (32 * c + 8 * (r >> 2) + (r & 3))) & 1ull);
+      if (lane == 16 * c + r) out[16 * c + r] = m;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Dense masked attention (bf16)
 // ---------------------------------------------------------------------------
 struct DenseArgs {
   const uint16_t* q; int64_t q_sb, q_st;
   const uint16_t* k; int64_t k_sb, k_st;
   const uint16_t* vt; int64_t vt_sb, vt_sh; int ldv;
-  const uint32_t* bits; int64_t b_sb, b_st;
+  const uint64_t* lm; int G, NT;          // lane masks [B][G][NT][32]
   const uint16_t* og; int64_t o_sb, o_st;
   const uint16_t* cos; const uint16_t* sin; int64_t cs_st;
   uint16_t* out; int64_t out_sb, out_st;
@@ -202,7 +231,9 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
   const int nkt = last_key / kDK + 1;
   const uint16_t* kbase = p.k + b * p.k_sb + hd * 128;
   const uint16_t* vtb = p.vt + b * p.vt_sb + hd * p.vt_sh;
-  const uint32_t* brow = p.bits + b * p.b_sb + (int64_t)qr * p.b_st;
+  // this wave's lane masks: group 4*qb + w (wave index made uniform for scalar loads)
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const uint64_t* lmw = p.lm + ((int64_t)b * p.G + 4 * qb + wu) * p.NT * 32;
 
   // staging: K tile = 64 keys x 16 chunks of 16 B, V^T tile = 128 rows x 8 chunks
   u32x4 kreg[4], vreg[4];
@@ -247,8 +278,7 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
     __syncthreads();
     if (kt + 1 < nkt) fetch(kt + 1);   // next tile's loads fly during this tile's math
 
-    // selection bits of this lane's keys, pre-shifted by its lane half
-    const uint64_t mb = (qrow < p.T ? *reinterpret_cast<const uint64_t*>(brow + 2 * kt) : 0ull) >> (4 * h);
+    const uint64_t* lmt = lmw + kt * 32;   // 32 slot masks of this tile
 
     // ---- S^T = K Q^T: two 32-key subtiles ----
     floatx16 sacc[2];
@@ -274,7 +304,7 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const bool sel = (mb >> (32 * c + 8 * (r >> 2) + (r & 3))) & 1ull;
+        const bool sel = __builtin_amdgcn_inverse_ballot_w64(lmt[16 * c + r]);
         sacc[c][r] = sel ? sacc[c][r] : -__builtin_inff();
         mx = fmaxf(mx, sacc[c][r]);
       }
@@ -396,6 +426,11 @@ extern "C" int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st
   return launch_status();
 }
 
+extern "C" size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv) {
+  if (B < 1 || T < 1 || Tkv < 1) return 0;
+  return (size_t)B * ((T + 31) / 32) * ((Tkv + 63) / 64) * 32 * sizeof(uint64_t);
+}
+
 extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                               const void* k, int64_t k_sb, int64_t k_st,
                               const void* vt, int64_t vt_sb, int64_t vt_sh, int ldv,
@@ -405,29 +440,39 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                               void* out, int64_t out_sb, int64_t out_st,
                               int B, int T, int Tkv, int H, int d, float scale,
                               int dtype, int flags, int causal,
+                              void* ws, size_t ws_bytes,
                               void* stream) {
-  if (!q || !k || !vt || !bits || !out) return GSA_ERR_NULL;
+  if (!q || !k || !vt || !bits || !out || !ws) return GSA_ERR_NULL;
   if (flags & ~(GSA_ATTN_ROPE_Q | GSA_ATTN_OUT_GATE)) return GSA_ERR_FLAGS;
   if ((flags & GSA_ATTN_ROPE_Q) && (!cos || !sin)) return GSA_ERR_NULL;
   if ((flags & GSA_ATTN_OUT_GATE) && !og) return GSA_ERR_NULL;
   if (dtype != GSA_DTYPE_BF16) return GSA_ERR_DTYPE;
   if (B < 1 || T < 1 || Tkv < 1 || d != 128 || H < 1 || H > 64) return GSA_ERR_SHAPE;
-  const int nkt = (Tkv + 63) / 64;
-  if (ldv < nkt * 64 || ldv % 64 != 0) return GSA_ERR_SHAPE;
+  const int NT = (Tkv + 63) / 64;
+  if (ldv < NT * 64 || ldv % 64 != 0) return GSA_ERR_SHAPE;
+  if (b_st < 2 * NT || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
+  if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
   const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
-  if ((int64_t)B * H * nqb > 0x7fffffffLL) return GSA_ERR_SHAPE;
+  const int G = nqb * (gsa::kDQ / 32);    // 32-row groups, padded to whole blocks
+  if ((int64_t)B * H * nqb > 0x7fffffffLL || (int64_t)B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
   if (!vec_ok(q, q_sb, q_st, dtype) || !vec_ok(k, k_sb, k_st, dtype) || !vec_ok(vt, vt_sb, vt_sh, dtype) ||
-      !vec_ok(out, out_sb, out_st, dtype) || !aligned(bits, 8) || (b_sb % 2) || (b_st % 2))
+      !vec_ok(out, out_sb, out_st, dtype) || !aligned(bits, 8) || (b_sb % 2) || (b_st % 2) || !aligned(ws, 8))
     return GSA_ERR_ALIGN;
   if ((flags & GSA_ATTN_OUT_GATE) && !vec_ok(og, o_sb, o_st, dtype)) return GSA_ERR_ALIGN;
   if ((flags & GSA_ATTN_ROPE_Q) && (!vec_ok(cos, 0, cs_st, dtype) || !vec_ok(sin, 0, cs_st, dtype)))
     return GSA_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint64_t* lm = static_cast<uint64_t*>(ws);
+  const int nwaves = B * G * NT;
+  hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((nwaves + 3) / 4), dim3(256), 0, s, bits, b_sb, b_st, T, G, NT,
+                     nwaves, lm);
+  int st = launch_status();
+  if (st) return st;
   gsa::DenseArgs a{static_cast<const uint16_t*>(q), q_sb, q_st, static_cast<const uint16_t*>(k), k_sb, k_st,
-                   static_cast<const uint16_t*>(vt), vt_sb, vt_sh, ldv, bits, b_sb, b_st,
+                   static_cast<const uint16_t*>(vt), vt_sb, vt_sh, ldv, lm, G, NT,
                    static_cast<const uint16_t*>(og), o_sb, o_st, static_cast<const uint16_t*>(cos),
                    static_cast<const uint16_t*>(sin), cs_st, static_cast<uint16_t*>(out), out_sb, out_st,
                    B, T, Tkv, H, nqb, scale * gsa::kLog2e, flags | (causal ? gsa::kDenseCausal : 0)};
-  hipLaunchKernelGGL(gsa::dense_attn_kernel, dim3(B * H * nqb), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     a);
+  hipLaunchKernelGGL(gsa::dense_attn_kernel, dim3(B * H * nqb), dim3(256), 0, s, a);
   return launch_status();
 }

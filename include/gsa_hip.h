@@ -200,12 +200,17 @@ int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel
  * Block-dense sparse attention on MFMA: the function of gsa_sparse_attn
  * (fused_sparse_attention, gsa_triton/gsa_opt.py:349-383, with the optional
  * RoPE(q) and G1 gate of gsa_opt.py:692-701,719-721) computed over whole
- * 64-key tiles with the selection applied as a bitmask (gsa_selection_mask).
+ * 64-key tiles with the selection applied as a bitmask (bits as written by
+ * gsa_indexer_select or gsa_selection_mask).
  * q, out, og [B,T,H,d]; k [B,Tkv,H,d] (RoPE'd); vt [B,H,d,ldv] as written by
  * gsa_prologue_vt (strides vt_sb, vt_sh per batch and head; rows of ldv).
- * causal != 0: key tiles after a 64-row query block's last row are skipped
- * (the selection must then be causal).  bf16 only; d == 128, 1 <= H <= 64.
+ * causal != 0: key tiles after a 128-row query block's last row are skipped
+ * (the selection must then be causal).  ws: caller-provided device workspace
+ * of at least gsa_dense_attn_workspace_bytes(B, T, Tkv) bytes (8-byte
+ * aligned), overwritten by each call.  bf16 only; d == 128, 1 <= H <= 64.
  */
+size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
+
 int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                    const void* k, int64_t k_sb, int64_t k_st,
                    const void* vt, int64_t vt_sb, int64_t vt_sh, int ldv,
@@ -215,6 +220,7 @@ int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                    void* out, int64_t out_sb, int64_t out_st,
                    int B, int T, int Tkv, int H, int d, float scale,
                    int dtype, int flags, int causal,
+                   void* ws, size_t ws_bytes,
                    void* stream);
 
 #ifdef __cplusplus

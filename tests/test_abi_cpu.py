@@ -105,7 +105,7 @@ def test_dense_path_validation(lib):
     g = lib.gsa_dense_attn
     ok = dict(q=P, qsb=0, qst=2048, k=P, ksb=0, kst=2048, vt=P, vtsb=0, vtsh=8192, ldv=64, bits=P, bsb=0, bst=2,
               og=P, osb=0, ost=2048, cos=P, sin=P, cst=128, out=P, outsb=0, outst=2048,
-              B=1, T=4, Tkv=4, H=16, d=128, scale=0.088, dtype=1, flags=3, causal=1)
+              B=1, T=4, Tkv=4, H=16, d=128, scale=0.088, dtype=1, flags=3, causal=1, ws=P, wsb=256)
 
     def call(**kw):
         a = dict(ok)
@@ -113,9 +113,13 @@ def test_dense_path_validation(lib):
         return g(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["vt"], a["vtsb"], a["vtsh"], a["ldv"],
                  a["bits"], a["bsb"], a["bst"], a["og"], a["osb"], a["ost"], a["cos"], a["sin"], a["cst"],
                  a["out"], a["outsb"], a["outst"], a["B"], a["T"], a["Tkv"], a["H"], a["d"], a["scale"],
-                 a["dtype"], a["flags"], a["causal"], None)
+                 a["dtype"], a["flags"], a["causal"], a["ws"], a["wsb"], None)
 
+    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 4) == 256
+    assert lib.gsa_dense_attn_workspace_bytes(2, 100, 130) == 2 * 4 * 3 * 256
     assert call(bits=None) == 1
+    assert call(ws=None) == 1
+    assert call(wsb=255) == 2                     # workspace too small
     assert call(dtype=0) == 3                     # bf16 only
     assert call(ldv=32) == 2                      # rows shorter than ceil(Tkv/64)*64
     assert call(flags=4) == 6
