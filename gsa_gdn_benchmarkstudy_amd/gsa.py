@@ -247,9 +247,11 @@ class GatedSparseAttention(nn.Module):
     """Drop-in replacement for gsa_ref/gsa_opt.GatedSparseAttention.
 
     Forward, per layer call:
-      1. one GEMM for the eight projections (weight padded to a multiple of 64
-         output columns; the slices are strided views, never copied);
-      2. indexer stream: gsa_indexer_select -- MFMA indexer fused with the
+      1. the indexer projections (one small GEMM over the fused weight's last,
+         zero-padded 64-aligned row block), then the q/k/v/gate GEMM; the slices
+         are strided views, never copied;
+      2. indexer stream (concurrent with the q/k/v/gate GEMM):
+         gsa_indexer_select -- MFMA indexer fused with the
          exact top-k, writing ascending int32 indices and per-row counts
          (the T x T score matrix is never stored) -- and, for the dense
          attention, gsa_selection_mask (the selection as a bitmask);
@@ -338,21 +340,35 @@ class GatedSparseAttention(nn.Module):
         return off
 
     # -- forward pieces (also used by tests) -------------------------------
-    def project(self, x: torch.Tensor):
-        """Fused GEMM; returns a dict of strided [B,T,...] views into one buffer."""
+    def project_indexer(self, x: torch.Tensor):
+        """GEMM of the indexer projections (idx_q, idx_k, idx_w: the fused weight's
+        last, zero-padded 64-aligned row block) -> dict of strided views."""
         B, T, D = x.shape
-        H, d = self.num_heads, self.d_head
         Hi, di = self.indexer.n_idx_heads, self.indexer.d_indexer
         w, b = self._get_fused_weight(x)
-        comb = F.linear(x, w, b)
         off = self._offsets()
-        v = {}
-        for n in ("q", "k", "v", "vg", "og"):
-            v[n] = comb[..., off[n]:off[n] + D].view(B, T, H, d)
-        v["iq"] = comb[..., off["iq"]:off["iq"] + Hi * di].view(B, T, Hi, di)
-        v["ik"] = comb[..., off["ik"]:off["ik"] + di]
-        v["iw"] = comb[..., off["iw"]:off["iw"] + Hi]
+        base = off["iq"]
+        comb = F.linear(x, w[base:], b[base:])
+        return {"iq": comb[..., :Hi * di].view(B, T, Hi, di),
+                "ik": comb[..., off["ik"] - base:off["ik"] - base + di],
+                "iw": comb[..., off["iw"] - base:off["iw"] - base + Hi],
+                "_ibuf": comb}
+
+    def project_main(self, x: torch.Tensor):
+        """GEMM of q, k, v and the two gate projections -> dict of strided views."""
+        B, T, D = x.shape
+        H, d = self.num_heads, self.d_head
+        w, b = self._get_fused_weight(x)
+        off = self._offsets()
+        comb = F.linear(x, w[:off["iq"]], b[:off["iq"]])
+        v = {n: comb[..., off[n]:off[n] + D].view(B, T, H, d) for n in ("q", "k", "v", "vg", "og")}
         v["_buf"] = comb
+        return v
+
+    def project(self, x: torch.Tensor):
+        """All eight projections -> dict of strided [B,T,...] views."""
+        v = self.project_indexer(x)
+        v.update(self.project_main(x))
         return v
 
     def select(self, views, T: int, indices: bool = True):
@@ -387,13 +403,13 @@ class GatedSparseAttention(nn.Module):
         dev = x.device
         cur = torch.cuda.current_stream(dev)
 
-        _range_push("gsa_hip/fused_gemm")
-        views = self.project(x)
-        _range_pop()
-
         dense = self.uses_dense(x.dtype)
 
-        # Track A: indexer + top-k (+ its bitmask) on the side stream
+        # Track A: indexer projections, then indexer + top-k (+ its bitmask) on
+        # the side stream, concurrent with the main projection GEMM
+        _range_push("gsa_hip/indexer_gemm")
+        views = self.project_indexer(x)
+        _range_pop()
         if self._indexer_stream is None or self._indexer_stream.device != dev:
             self._indexer_stream = torch.cuda.Stream(device=dev)
         side = self._indexer_stream
@@ -402,6 +418,10 @@ class GatedSparseAttention(nn.Module):
             _range_push("gsa_hip/indexer_select")
             bits, idx, cnt = self.select(views, T, indices=not dense)
             _range_pop()
+
+        _range_push("gsa_hip/main_gemm")
+        views.update(self.project_main(x))
+        _range_pop()
 
         # Track B: RoPE(k) and the value gate on the current stream
         _range_push("gsa_hip/prologue")
@@ -417,7 +437,7 @@ class GatedSparseAttention(nn.Module):
         for t in (idx, cnt, bits):
             if t is not None:
                 t.record_stream(cur)
-        views["_buf"].record_stream(side)
+        views["_ibuf"].record_stream(side)
 
         _range_push("gsa_hip/sparse_attn")
         ev = None
