@@ -135,14 +135,16 @@ __global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restri
   const int row = 32 * g + i;
   uint64_t word = row < T ? *reinterpret_cast<const uint64_t*>(bits + b * b_sb + (int64_t)row * b_st + 2 * kt) : 0ull;
   word >>= 4 * h;
-  uint64_t* out = lm + ((int64_t)bg * NT + kt) * 32;
+  // lane s collects slot s's mask; lanes 0..31 then write 256 contiguous bytes
+  uint64_t mine = 0ull;
 #pragma unroll
   for (int c = 0; c < 2; ++c)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const uint64_t m = ballot64((word >> (32 * c + 8 * (r >> 2) + (r & 3))) & 1ull);
-      if (lane == 16 * c + r) out[16 * c + r] = m;
+      mine = lane == 16 * c + r ? m : mine;
     }
+  if (lane < 32) lm[((int64_t)bg * NT + kt) * 32 + lane] = mine;
 }
 
 // ---------------------------------------------------------------------------

@@ -284,6 +284,7 @@ class GatedSparseAttention(nn.Module):
 
         self._fused_weight: Optional[torch.Tensor] = None
         self._fused_bias: Optional[torch.Tensor] = None
+        self._idx_bias32: Optional[torch.Tensor] = None
         self._proj_sizes = [
             hidden_size, hidden_size, hidden_size, hidden_size, hidden_size,
             n_idx_heads * d_indexer, d_indexer, n_idx_heads,
@@ -304,6 +305,7 @@ class GatedSparseAttention(nn.Module):
     def _drop_fused(self) -> None:
         self._fused_weight = None
         self._fused_bias = None
+        self._idx_bias32 = None
 
     def fuse_projections(self) -> None:
         """Build the fused, padded projection weight/bias.  Call after load_state_dict()."""
@@ -324,6 +326,8 @@ class GatedSparseAttention(nn.Module):
         bias[off["iw"]:off["iw"] + self.indexer.n_idx_heads] = self.indexer.idx_w_proj.bias.detach()
         self._fused_weight = w.contiguous()
         self._fused_bias = bias
+        # fp32 copy of the indexer bias for the kernels (built here, not per call)
+        self._idx_bias32 = self.indexer.idx_bias.detach().float().contiguous()
 
     def _get_fused_weight(self, like: Optional[torch.Tensor] = None):
         fw = self._fused_weight
@@ -378,7 +382,9 @@ class GatedSparseAttention(nn.Module):
         (ascending int32, per-row count) only when ``indices``.
         """
         k_eff = self.topk_selector.k_effective(T)
-        bias = self.indexer.idx_bias.detach().float().contiguous()
+        bias = self._idx_bias32
+        if bias is None or bias.device != views["iq"].device:
+            bias = self._idx_bias32 = self.indexer.idx_bias.detach().float().contiguous()
         return _abi.indexer_select(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale, k_eff,
                                    indices=indices)
 
