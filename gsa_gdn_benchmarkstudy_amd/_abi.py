@@ -34,6 +34,7 @@ EXPORTS = (
     "gsa_abi_version", "gsa_status_string", "gsa_indexer_scores", "gsa_topk_select",
     "gsa_indexer_select", "gsa_prologue", "gsa_sparse_attn", "gsa_prologue_vt",
     "gsa_selection_mask", "gsa_dense_attn", "gsa_dense_attn_workspace_bytes",
+    "gsa_indexer_select_workspace_bytes",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -45,7 +46,9 @@ _PROTOS = {
                             _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp], _i32),
     "gsa_topk_select": ([_vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "gsa_indexer_select": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
-                            _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp, _vp], _i32),
+                            _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp,
+                            _vp, ctypes.c_size_t, _vp], _i32),
+    "gsa_indexer_select_workspace_bytes": ([_i32, _i32], ctypes.c_size_t),
     "gsa_prologue": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
                       _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
     "gsa_sparse_attn": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
@@ -176,13 +179,18 @@ def topk_select(scores: torch.Tensor, k_eff: int, order: int = ORDER_INDEX_ASC,
     return idx, cnt, mask
 
 
+def indexer_select_workspace_bytes(B: int, T: int) -> int:
+    return int(load().gsa_indexer_select_workspace_bytes(B, T))
+
+
 def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int, indices: bool = True,
-                   bits: Optional[torch.Tensor] = None):
+                   bits: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None):
     """Fused indexer + exact top-k.
 
     Returns (bits, idx, count): the selection bitmask int32 [B,T,W] (W =
     2*ceil(T/64)) and, when ``indices``, ascending int32 indices [B,T,k_eff]
-    and counts int32 [B,T] (else None, None).
+    and counts int32 [B,T] (else None, None).  ``ws``: optional workspace
+    (uint8 device tensor of at least indexer_select_workspace_bytes(B, T)).
     """
     lib = load()
     _need_cuda(q_idx, k_idx, w, bias32)
@@ -199,10 +207,15 @@ def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int, indices: b
     if indices:
         idx = torch.empty(B, T, k_eff, device=q_idx.device, dtype=torch.int32)
         cnt = torch.empty(B, T, device=q_idx.device, dtype=torch.int32)
-    qs, ks, ws = _rows(q_idx, Hi * di), _rows(k_idx, di), _rows(w, Hi)
-    st = lib.gsa_indexer_select(_ptr(q_idx), *qs, _ptr(k_idx), *ks, _ptr(w), *ws, _ptr(bias32),
+    nbytes = lib.gsa_indexer_select_workspace_bytes(B, T)
+    if ws is None:
+        ws = torch.empty(nbytes, device=q_idx.device, dtype=torch.uint8)
+    _expect(ws.numel() * ws.element_size() >= nbytes and ws.is_contiguous(), "workspace too small")
+    qs, ks, wst = _rows(q_idx, Hi * di), _rows(k_idx, di), _rows(w, Hi)
+    st = lib.gsa_indexer_select(_ptr(q_idx), *qs, _ptr(k_idx), *ks, _ptr(w), *wst, _ptr(bias32),
                                 float(scale), B, T, Hi, di, int(k_eff), dtype_code(q_idx.dtype),
-                                _ptr(bits), bits.stride(0), bits.stride(1), _ptr(idx), _ptr(cnt), _stream(q_idx))
+                                _ptr(bits), bits.stride(0), bits.stride(1), _ptr(idx), _ptr(cnt),
+                                _ptr(ws), nbytes, _stream(q_idx))
     _check(st, "gsa_indexer_select")
     return bits, idx, cnt
 

@@ -26,6 +26,9 @@ CXX_SOURCES = ("abi.cpp",)
 # otherwise form v_pk_{add,mul,fma}_f32 from ordinary float code.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON_FLAGS = ["-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-function"]
+# The indexer's MFMA results feed VALU epilogues directly: keep them in arch
+# VGPRs instead of AGPRs (saves a v_accvgpr_read per result element).
+FILE_FLAGS = {"indexer.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
 
 
 def hipcc() -> str:
@@ -57,7 +60,7 @@ def build_library(verbose: bool = False, jobs: int = 4) -> str:
         obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
         cmd = [cc, f"--offload-arch={ARCH}", *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
         if src.endswith(".hip"):
-            cmd[2:2] = DEVICE_FLAGS
+            cmd[2:2] = DEVICE_FLAGS + FILE_FLAGS.get(src, [])
         else:
             cmd = [cc, *COMMON_FLAGS, "-x", "c++", "-c", os.path.join(CSRC, src), "-o", obj]
         jobs_list.append(cmd)

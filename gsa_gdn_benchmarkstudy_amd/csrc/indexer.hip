@@ -177,31 +177,41 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 }
 
 // ---------------------------------------------------------------------------
-// Fused indexer + exact top-k (never stores the score matrix).
+// Fused indexer + exact top-k.
 //
 // Output: the selection as a bitmask, bits[b][t] bit j set iff key j is one
 // of row t's selected keys (W = 2*ceil(T/64) uint32 words per row; words past
 // row t's causal range are zero).  One 256-thread block per 16-row group,
 // heaviest groups first; its 4 waves take the group's causal 16-key tiles
 // round-robin and share the row state in LDS.  Rows with t+1 <= k select
-// every causal key.  For the others the scores are computed twice:
-//   pass 1  value-linear histogram, bin = floor(s * NB / sum_h sigmoid(w_h))
-//           -> the bin b1 holding the k-th largest score and the rank of the
-//           k-th largest inside it;
-//   pass 2  entries in bins above b1 are selected: ballot -> one 16-bit chunk
-//           of the row's bitmask per 16-key tile; entries in b1 (at most
-//           kCap per row) are collected as (key, index);
+// every causal key.  For the others:
+//   pass 1  MFMA scores -> value-linear histogram, bin = floor(s * NB /
+//           sum_h sigmoid(w_h)), and every score tile is stored to the
+//           workspace -> the bin b1 holding the k-th largest score and the
+//           rank of the k-th largest inside it;
+//   pass 2  the stored scores are read back: entries in bins above b1 are
+//           selected (ballots -> one 64-bit word of the row's bitmask per 4
+//           tiles); entries in b1 (at most kWCap per row and wave) are
+//           collected as (key, index);
 //   resolve exact MSB-first radix select among a row's candidates -> the
 //           threshold key theta and how many entries equal to theta to take,
 //           lowest indices first; winning candidates are OR-ed into the mask.
-// A bin holding more than kCap entries (degenerate scores, e.g. all equal)
-// falls back to four 8-bit radix passes over the bin, then one ordered pass
-// by a single wave marks the winners.
+// A bin holding more candidates than fit (degenerate scores, e.g. all equal)
+// falls back to four 8-bit radix passes over the stored scores of the bin,
+// then one ordered pass by a single wave marks the winners.
+//
+// Workspace: group g of batch b owns (g+1) consecutive 1 KiB score tiles
+// starting at tile b*tri(G) + tri(g), tri(n) = n(n+1)/2, G = ceil(T/16);
+// lane l of the wave that computes a tile stores its four output slots
+// (rows 4*(l/16)+e, column l%16) as floats 4l .. 4l+3, the layout it reads
+// back.
 // ---------------------------------------------------------------------------
 constexpr int kNB = 512;                 // histogram bins per row
 constexpr int kCap = 512;                // candidates per row
 constexpr int kHStride = kNB + 1;        // odd stride: one bin of 16 rows in distinct banks
 constexpr int kGroupWaves = 4;
+constexpr int kWCap = kCap / kGroupWaves;  // candidates per row and wave
+constexpr int kTile = 256;               // floats per stored 16x16 score tile
 
 enum RowMode : int { kNone = 0, kTrivial = 1, kActive = 2, kResolved = 3, kOverflow = 4 };
 
@@ -217,10 +227,10 @@ __device__ __forceinline__ uint16_t prefix_chunk(int row, int tile) {
 
 template <typename T>
 __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff, uint32_t* bits,
-                                                           int64_t b_sb, int64_t b_st) {
+                                                           int64_t b_sb, int64_t b_st, float* ws) {
   __shared__ uint32_t sh[16 * kHStride];   // histogram, then candidate keys
   __shared__ uint32_t sh_idx[16 * kCap];   // candidate key indices
-  __shared__ uint32_t sh_cnt[16];
+  __shared__ uint32_t sh_wcnt[16 * kGroupWaves];
   __shared__ int st_mode[16], st_b1[16], st_need[16];
   __shared__ uint32_t st_key[16];
   __shared__ int st_any[2];                // [0] any active row, [1] any overflow
@@ -234,12 +244,12 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
   uint32_t* bbase = bits + b * b_sb;
   uint16_t* b16 = reinterpret_cast<uint16_t*>(bbase);
   const int64_t row16 = 2 * b_st;          // uint16 chunks per row
+  float* wsg = ws + ((int64_t)b * ngroups * (ngroups + 1) / 2 + (int64_t)rg_idx * (rg_idx + 1) / 2) * kTile;
 
   if (tid < 16) {
     const int row = r0 + tid;
     st_mode[tid] = row >= p.T ? kNone : (row + 1 > k_eff ? kActive : kTrivial);
     st_need[tid] = k_eff;
-    sh_cnt[tid] = 0u;
   }
   if (tid < 2) st_any[tid] = 0;
   __syncthreads();
@@ -271,37 +281,28 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
 
   RowGroup<T> rgp;
   rgp.init(p, b, r0, lane);
-  int mode[4], b1[4];
+  bool act[4];
+  int b1[4];
   float inv_w[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    mode[e] = st_mode[4 * g + e];
+    act[e] = st_mode[4 * g + e] == kActive;
     const float smax = ((rgp.a[e][0] + rgp.a[e][1]) + rgp.a[e][2]) + rgp.a[e][3];
     inv_w[e] = (float)kNB / (smax * 1.0009765625f + 1e-30f);
     b1[e] = 0;
   }
-
-  typename Mfma<T>::Op kb[Mfma<T>::kSteps], kn[Mfma<T>::kSteps];
-  // This wave's tiles: wave, wave+4, ...; f(e, row, col, tile, valid, score).
-  auto sweep = [&](auto&& f) {
-    int t = wave;
-    if (t < ntl) rgp.load_keys(t * 16, p.T, lane, kn);
-    for (; t < ntl; t += kGroupWaves) {
+  // Lane 16g+e (e < 4) writes the mask chunks of row 4g+e.
+  const int own_row = r0 + 4 * g + (lr & 3);
+  const bool own_act = lr < 4 && st_mode[4 * g + (lr & 3)] == kActive;
+  auto slot_valid = [&](int col, bool (&valid)[4]) {
 #pragma unroll
-      for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = kn[s];
-      if (t + kGroupWaves < ntl) rgp.load_keys((t + kGroupWaves) * 16, p.T, lane, kn);
-      floatx4 acc[kHi];
-      rgp.mma(kb, acc);
-      const int col = t * 16 + lr;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = r0 + 4 * g + e;
-        const bool valid = mode[e] == kActive && col <= row;
-        f(e, row, col, t, valid, valid ? rgp.score(acc, e) : 0.f);
-      }
-    }
+    for (int e = 0; e < 4; ++e) valid[e] = act[e] && col <= r0 + 4 * g + e;
   };
 
+  // ---- pass 1: scores -> histogram + workspace ------------------------------
+  // This wave's tiles: wave, wave+4, ...  Scores are computed for every slot
+  // (no divergent branch around the epilogue); invalid slots count into bin
+  // kNB, the row's padding slot, which no scan reads.
   auto scan_row = [&](int rl, int& nd) -> int {     // top-down cumulative search
     int cum = 0, bsel = 0;
     for (int bin = kNB - 1; bin >= 0; --bin) {
@@ -317,11 +318,29 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
     __syncthreads();
   };
 
-  // ---- pass 1: histogram ---------------------------------------------------
   zero_hist();
-  sweep([&](int e, int, int, int, bool valid, float s) {
-    if (valid) atomicAdd(&sh[(4 * g + e) * kHStride + bin_of(s, inv_w[e])], 1u);
-  });
+  {
+    typename Mfma<T>::Op kb[Mfma<T>::kSteps], kn[Mfma<T>::kSteps];
+    int t = wave;
+    if (t < ntl) rgp.load_keys(t * 16, p.T, lane, kn);
+    for (; t < ntl; t += kGroupWaves) {
+#pragma unroll
+      for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = kn[s];
+      if (t + kGroupWaves < ntl) rgp.load_keys((t + kGroupWaves) * 16, p.T, lane, kn);
+      floatx4 acc[kHi];
+      rgp.mma(kb, acc);
+      bool valid[4];
+      slot_valid(t * 16 + lr, valid);
+      floatx4 sc;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sc[e] = rgp.score(acc, e);
+        const int bn = valid[e] ? bin_of(sc[e], inv_w[e]) : kNB;
+        atomicAdd(&sh[(4 * g + e) * kHStride + bn], 1u);
+      }
+      *reinterpret_cast<floatx4*>(wsg + t * kTile + lane * 4) = sc;
+    }
+  }
   __syncthreads();
   if (tid < 16 && st_mode[tid] == kActive) {
     int nd = st_need[tid];
@@ -333,63 +352,163 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
   for (int e = 0; e < 4; ++e) b1[e] = st_b1[4 * g + e];
   __syncthreads();   // sh is reused for candidate keys below
 
-  // ---- pass 2: bins above b1 -> mask chunks; bin b1 -> candidates ------------
-  sweep([&](int e, int row, int col, int t, bool valid, float s) {
-    const int bn = bin_of(s, inv_w[e]);
-    const bool sel = valid && bn > b1[e];
-    if (valid && bn == b1[e]) {
-      const int rl = 4 * g + e;
-      const uint32_t pos = atomicAdd(&sh_cnt[rl], 1u);
-      if (pos < (uint32_t)kCap) {
-        sh[rl * kHStride + pos] = score_key(s);
-        sh_idx[rl * kCap + pos] = (uint32_t)col;
+  // Replay of the stored tiles in quads of 4 consecutive tiles (quad j =
+  // tiles 4j .. 4j+3, one 64-key word pair of the mask).  Each wave takes
+  // runs of kRun consecutive quads, runs round-robin over the waves, and
+  // issues all loads of a run before using any: nothing loaded stays live
+  // across an iteration, so the waits before each quad count only the loads
+  // issued after it.  Tile indices past the last tile re-read the last one
+  // (always in bounds) and every quad of a run is processed: a tile past the
+  // diagonal has no valid slot (its columns lie after every row of the
+  // group), so a quad j >= nquad contributes nothing, and fq must not store
+  // for it.
+  constexpr int kRun = 3;
+  const int nquad = (ntl + 3) >> 2;
+  auto load_quad = [&](int j, floatx4 (&v)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = min(4 * j + u, ntl - 1);
+      v[u] = *reinterpret_cast<const floatx4*>(wsg + t * kTile + lane * 4);
+    }
+  };
+  // f(quad, u, col, valid[4], score[4]) per tile, then fq(quad) per quad.
+  auto replay = [&](auto&& f, auto&& fq) {
+    for (int c = wave; kRun * c < nquad; c += kGroupWaves) {
+      floatx4 qv[kRun][4];
+#pragma unroll
+      for (int r = 0; r < kRun; ++r) load_quad(kRun * c + r, qv[r]);
+#pragma unroll
+      for (int r = 0; r < kRun; ++r) {
+        const int j = kRun * c + r;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int col = (4 * j + u) * 16 + lr;
+          bool valid[4];
+          slot_valid(col, valid);
+          const float sc[4] = {qv[r][u][0], qv[r][u][1], qv[r][u][2], qv[r][u][3]};
+          f(j, u, col, valid, sc);
+        }
+        fq(j);
       }
     }
-    const uint64_t m = ballot64(sel);
-    if (lr == 0 && mode[e] == kActive) b16[row * row16 + t] = (uint16_t)(m >> (16 * g));
-  });
-  __threadfence();
+  };
+
+  // ---- pass 2: bins above b1 -> mask words; bin b1 -> candidates -------------
+  // Candidates of row 4g+e found by this wave go to its own region of the
+  // row (kWCap slots), positions from a per-wave count: no atomics.  Lane
+  // 16g+e assembles row 4g+e's 64-bit mask word of each quad.
+  int wc[4] = {0, 0, 0, 0};
+  const uint32_t below = (1u << lr) - 1u;
+  uint64_t word = 0;
+  replay(
+      [&](int, int u, int col, const bool (&valid)[4], const float (&sc)[4]) {
+        uint64_t m[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int bn = bin_of(sc[e], inv_w[e]);
+          m[e] = ballot64(valid[e] && bn > b1[e]);
+          const bool cand = valid[e] && bn == b1[e];
+          const uint64_t cm = ballot64(cand);
+          if (cm) {
+            const uint32_t gm = (uint32_t)(cm >> (16 * g)) & 0xffffu;
+            const int pos = wc[e] + __popc(gm & below);
+            if (cand && pos < kWCap) {
+              const int rl = 4 * g + e;
+              sh[rl * kHStride + wave * kWCap + pos] = score_key(sc[e]);
+              sh_idx[rl * kCap + wave * kWCap + pos] = (uint32_t)col;
+            }
+            wc[e] += __popc(gm);
+          }
+        }
+        const uint64_t me = (lr & 2) ? ((lr & 1) ? m[3] : m[2]) : ((lr & 1) ? m[1] : m[0]);
+        word |= ((me >> (16 * g)) & 0xffffull) << (16 * u);
+      },
+      [&](int j) {
+        if (own_act && j < nquad) reinterpret_cast<uint64_t*>(bbase + (int64_t)own_row * b_st)[j] = word;
+        word = 0;
+      });
+  if (lr == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sh_wcnt[(4 * g + e) * kGroupWaves + wave] = (uint32_t)wc[e];
+  }
+  // The resolve's atomics below come from waves of this block only: the
+  // barrier (a workgroup-scope release/acquire) orders the mask stores above
+  // before them.  A device-scope fence here would write back the whole L2.
   __syncthreads();
 
   // ---- resolve: wave w takes rows 4w .. 4w+3 ----------------------------------
+  // Candidate slot i*64 + lane lies in region i/2 at position (i%2)*64 + lane.
   for (int q = 0; q < 4; ++q) {
     const int rl = 4 * wave + q;
     if (st_mode[rl] != kActive) continue;
-    const int n = (int)sh_cnt[rl];
-    if (n > kCap) {
+    int nw[kGroupWaves];
+    bool ovf = false;
+#pragma unroll
+    for (int w = 0; w < kGroupWaves; ++w) {
+      nw[w] = (int)sh_wcnt[rl * kGroupWaves + w];
+      ovf |= nw[w] > kWCap;
+    }
+    if (ovf) {
       if (lane == 0) { st_mode[rl] = kOverflow; st_any[1] = 1; }
       continue;
     }
-    uint32_t cv[kCap / 64], ci[kCap / 64];
+    constexpr int kSlots = kCap / 64;
+    uint32_t cv[kSlots], ci[kSlots];
+    bool cvalid[kSlots], used[kSlots];
+    uint32_t kor = 0u, kand = ~0u;
 #pragma unroll
-    for (int i = 0; i < kCap / 64; ++i) {
-      const int c = i * 64 + lane;
-      cv[i] = c < n ? sh[rl * kHStride + c] : 0u;
-      ci[i] = c < n ? sh_idx[rl * kCap + c] : 0u;
+    for (int i = 0; i < kSlots; ++i) {
+      const int w = i >> 1, pos = (i & 1) * 64 + lane;
+      used[i] = (i & 1) * 64 < nw[w];
+      cvalid[i] = pos < nw[w];
+      cv[i] = cvalid[i] ? sh[rl * kHStride + w * kWCap + pos] : 0u;
+      ci[i] = cvalid[i] ? sh_idx[rl * kCap + w * kWCap + pos] : 0u;
+      if (cvalid[i]) { kor |= cv[i]; kand &= cv[i]; }
+    }
+    // Bits on which every candidate agrees are part of theta; the radix
+    // select starts at the highest bit on which they differ.
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      kor |= (uint32_t)__shfl_xor((int)kor, o, 64);
+      kand &= (uint32_t)__shfl_xor((int)kand, o, 64);
     }
     int k = st_need[rl];
-    uint32_t prefix = 0u, pmask = 0u;
-    for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t diff = kor ^ kand;
+    const int top = diff ? 31 - __builtin_clz(diff) : -1;
+    uint32_t pmask = top >= 31 ? 0u : ~0u << (top + 1);
+    uint32_t prefix = kand & pmask;
+    for (int bit = top; bit >= 0; --bit) {
       const uint32_t tm = pmask | (1u << bit), tv = prefix | (1u << bit);
       int c = 0;
 #pragma unroll
-      for (int i = 0; i < kCap / 64; ++i) c += __popcll(ballot64((i * 64 + lane) < n && (cv[i] & tm) == tv));
+      for (int i = 0; i < kSlots; ++i)
+        if (used[i]) c += __popcll(ballot64(cvalid[i] && (cv[i] & tm) == tv));
       if (c >= k) prefix = tv; else k -= c;
       pmask = tm;
     }
-    // winners: key > theta, or key == theta among the k lowest indices of the ties
+    // winners: key > theta, or key == theta among the k lowest indices of the
+    // ties (all of them when there are at most k)
+    int ties = 0;
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i)
+      if (used[i]) ties += __popcll(ballot64(cvalid[i] && cv[i] == prefix));
     const int row = r0 + rl;
     uint32_t* brow = bbase + (int64_t)row * b_st;
 #pragma unroll
-    for (int i = 0; i < kCap / 64; ++i) {
-      const int c = i * 64 + lane;
-      if (c >= n) continue;
+    for (int i = 0; i < kSlots; ++i) {
+      if (!used[i] || !cvalid[i]) continue;
       bool win = cv[i] > prefix;
       if (cv[i] == prefix) {
-        int rank = 0;
-        for (int o = 0; o < n; ++o)
-          rank += (sh[rl * kHStride + o] == prefix && sh_idx[rl * kCap + o] < ci[i]) ? 1 : 0;
-        win = rank < k;
+        if (ties <= k) {
+          win = true;
+        } else {
+          int rank = 0;
+          for (int w = 0; w < kGroupWaves; ++w)
+            for (int o = 0; o < nw[w]; ++o)
+              rank += (sh[rl * kHStride + w * kWCap + o] == prefix &&
+                       sh_idx[rl * kCap + w * kWCap + o] < ci[i]) ? 1 : 0;
+          win = rank < k;
+        }
       }
       if (win) atomicOr(&brow[ci[i] >> 5], 1u << (ci[i] & 31));
     }
@@ -397,23 +516,28 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
   __syncthreads();
   if (!st_any[1]) return;
 
-  // ---- overflow rows: radix passes over the keys of bin b1 --------------------
+  // ---- overflow rows: radix passes over the stored scores of bin b1 -----------
   if (tid < 16 && st_mode[tid] == kOverflow) st_key[tid] = 0u;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) mode[e] = st_mode[4 * g + e] == kOverflow ? kActive : kNone;
+  for (int e = 0; e < 4; ++e) act[e] = st_mode[4 * g + e] == kOverflow;
   for (int level = 0; level < 4; ++level) {
     uint32_t pre[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) pre[e] = st_key[4 * g + e];
     const int hi_shift = 32 - 8 * level, lo_shift = 24 - 8 * level;
     zero_hist();
-    sweep([&](int e, int, int, int, bool valid, float s) {
-      if (valid && bin_of(s, inv_w[e]) == b1[e]) {
-        const uint32_t key = score_key(s);
-        if (level == 0 || (key >> hi_shift) == pre[e])
-          atomicAdd(&sh[(4 * g + e) * kHStride + ((key >> lo_shift) & 255u)], 1u);
-      }
-    });
+    replay(
+        [&](int, int, int, const bool (&valid)[4], const float (&sc)[4]) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (valid[e] && bin_of(sc[e], inv_w[e]) == b1[e]) {
+              const uint32_t key = score_key(sc[e]);
+              if (level == 0 || (key >> hi_shift) == pre[e])
+                atomicAdd(&sh[(4 * g + e) * kHStride + ((key >> lo_shift) & 255u)], 1u);
+            }
+          }
+        },
+        [](int) {});
     __syncthreads();
     if (tid < 16 && st_mode[tid] == kOverflow) {
       int cum = 0, d = 0, nd = st_need[tid];
@@ -427,7 +551,8 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
     }
     __syncthreads();
   }
-  // wave 0 marks the winners of the overflow rows in key order (tie ranks need order)
+  // wave 0 marks the winners of the overflow rows in key order (tie ranks need
+  // order); every wave's stored tiles are visible after the barriers above
   if (wave == 0) {
     uint32_t theta[4];
     int tie_need[4], tie_seen[4];
@@ -438,21 +563,16 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
       tie_seen[e] = 0;
     }
     const uint64_t gmask = 0xffffull << (16 * g);
-    rgp.load_keys(0, p.T, lane, kn);
     for (int t = 0; t < ntl; ++t) {
-#pragma unroll
-      for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = kn[s];
-      if (t + 1 < ntl) rgp.load_keys((t + 1) * 16, p.T, lane, kn);
-      floatx4 acc[kHi];
-      rgp.mma(kb, acc);
+      const floatx4 v = *reinterpret_cast<const floatx4*>(wsg + t * kTile + lane * 4);
       const int col = t * 16 + lr;
+      bool valid[4];
+      slot_valid(col, valid);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = r0 + 4 * g + e;
-        const bool valid = mode[e] == kActive && col <= row;
-        const float s = valid ? rgp.score(acc, e) : 0.f;
-        const bool inbin = valid && bin_of(s, inv_w[e]) == b1[e];
-        const uint32_t key = score_key(s);
+        const bool inbin = valid[e] && bin_of(v[e], inv_w[e]) == b1[e];
+        const uint32_t key = score_key(v[e]);
         const bool tie = inbin && key == theta[e];
         const uint64_t tmask = ballot64(tie) & gmask;
         const int trank = tie_seen[e] + count_below(tmask);
@@ -567,6 +687,12 @@ extern "C" int gsa_indexer_scores(const void* q_idx, int64_t q_sb, int64_t q_st,
   return launch_status();
 }
 
+extern "C" size_t gsa_indexer_select_workspace_bytes(int B, int T) {
+  if (B < 1 || T < 1) return 0;
+  const size_t g = (size_t)((T + 15) / 16);
+  return (size_t)B * (g * (g + 1) / 2) * gsa::kTile * sizeof(float);
+}
+
 extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                                   const void* k_idx, int64_t k_sb, int64_t k_st,
                                   const void* w, int64_t w_sb, int64_t w_st,
@@ -574,10 +700,10 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                                   int B, int T, int Hi, int di, int k_eff, int dtype,
                                   uint32_t* bits, int64_t b_sb, int64_t b_st,
                                   int32_t* idx_out, int32_t* count_out,
-                                  void* stream) {
+                                  void* ws, size_t ws_bytes, void* stream) {
   int st = check_indexer_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype);
   if (st) return st;
-  if (!bits) return GSA_ERR_NULL;
+  if (!bits || !ws) return GSA_ERR_NULL;
   if ((idx_out == nullptr) != (count_out == nullptr)) return GSA_ERR_NULL;
   if (k_eff < 1 || k_eff > T) return GSA_ERR_K;
   const int W = 2 * ((T + 63) / 64);
@@ -585,15 +711,17 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
   if (!aligned(bits, 8) || (b_st % 2) || (b_sb % 2)) return GSA_ERR_ALIGN;
   if (idx_out && (!aligned(idx_out, 4) || !aligned(count_out, 4))) return GSA_ERR_ALIGN;
   if ((int64_t)B * T > 0x7fffffffLL) return GSA_ERR_SHAPE;
+  if (ws_bytes < gsa_indexer_select_workspace_bytes(B, T)) return GSA_ERR_SHAPE;
+  if (!aligned(ws, 16)) return GSA_ERR_ALIGN;
   gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
   const int ngroups = (T + 15) / 16;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == GSA_DTYPE_BF16)
     hipLaunchKernelGGL(gsa::indexer_bits_kernel<uint16_t>, dim3(B * ngroups), dim3(256), 0, s, a, k_eff, bits,
-                       b_sb, b_st);
+                       b_sb, b_st, static_cast<float*>(ws));
   else
     hipLaunchKernelGGL(gsa::indexer_bits_kernel<float>, dim3(B * ngroups), dim3(256), 0, s, a, k_eff, bits,
-                       b_sb, b_st);
+                       b_sb, b_st, static_cast<float*>(ws));
   st = launch_status();
   if (st || !idx_out) return st;
   hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_eff,

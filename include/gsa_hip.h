@@ -99,7 +99,7 @@ int gsa_topk_select(const float* scores, int64_t s_sb, int64_t s_st,
                     void* stream);
 
 /*
- * Indexer and selector fused: the [B,T,T] score matrix is never stored.
+ * Indexer and selector fused.
  * Replaces the indexer track of the optimized forward (gsa_triton/gsa_opt.py:
  * 663-677: fused_gated_indexer + AdaptiveTopKSelector + ascending sort).
  * Selects exactly what gsa_indexer_scores followed by gsa_topk_select
@@ -109,8 +109,14 @@ int gsa_topk_select(const float* scores, int64_t s_sb, int64_t s_st,
  * takes.  When idx_out and count_out are given it also writes, like
  * GSA_ORDER_INDEX_ASC: idx_out int32 [B,T,k_eff] = row t's min(t+1, k_eff)
  * selected keys ascending, followed by t+1, t+2, ...; count_out int32 [B,T].
+ * ws: caller-provided device workspace of at least
+ * gsa_indexer_select_workspace_bytes(B, T) bytes (16-byte aligned),
+ * overwritten by each call: the causal score tiles, stored once and read
+ * back instead of recomputed (B * G(G+1)/2 KiB, G = ceil(T/16)).
  * Supported: Hi == 4, di == 64, 1 <= k_eff <= T.
  */
+size_t gsa_indexer_select_workspace_bytes(int B, int T);
+
 int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                        const void* k_idx, int64_t k_sb, int64_t k_st,
                        const void* w, int64_t w_sb, int64_t w_st,
@@ -118,6 +124,7 @@ int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                        int B, int T, int Hi, int di, int k_eff, int dtype,
                        uint32_t* bits, int64_t b_sb, int64_t b_st,
                        int32_t* idx_out, int32_t* count_out,
+                       void* ws, size_t ws_bytes,
                        void* stream);
 
 /*

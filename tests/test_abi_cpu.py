@@ -78,11 +78,12 @@ def test_indexer_scores_validation(lib):
 
 def _select(lib, **kw):
     a = dict(q=P, qsb=0, qst=256, k=P, ksb=0, kst=64, w=P, wsb=0, wst=4, bias=P, scale=0.125,
-             B=1, T=32, Hi=4, di=64, k_eff=8, dtype=1, bits=P, bsb=0, bst=2, idx=P, cnt=P)
+             B=1, T=32, Hi=4, di=64, k_eff=8, dtype=1, bits=P, bsb=0, bst=2, idx=P, cnt=P, ws=P, nws=3072)
     a.update(kw)
     return lib.gsa_indexer_select(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["w"], a["wsb"],
                                   a["wst"], a["bias"], a["scale"], a["B"], a["T"], a["Hi"], a["di"],
-                                  a["k_eff"], a["dtype"], a["bits"], a["bsb"], a["bst"], a["idx"], a["cnt"], None)
+                                  a["k_eff"], a["dtype"], a["bits"], a["bsb"], a["bst"], a["idx"], a["cnt"],
+                                  a["ws"], a["nws"], None)
 
 
 def test_indexer_select_validation(lib):
@@ -95,6 +96,14 @@ def test_indexer_select_validation(lib):
     assert _select(lib, k=MIS) == 4
     assert _select(lib, bst=1) == 2               # fewer words than 2*ceil(T/64)
     assert _select(lib, bits=P + 4) == 4          # rows must be 8-byte aligned
+    assert _select(lib, ws=None) == 1
+    assert _select(lib, nws=3071) == 2            # score workspace too small
+    assert _select(lib, ws=P + 8) == 4
+    # one 1 KiB tile per causal (16-row group, 16-key tile) pair
+    assert lib.gsa_indexer_select_workspace_bytes(1, 32) == 3 * 1024
+    assert lib.gsa_indexer_select_workspace_bytes(2, 100) == 2 * 28 * 1024
+    assert lib.gsa_indexer_select_workspace_bytes(1, 65536) == 4096 * 4097 // 2 * 1024
+    assert lib.gsa_indexer_select_workspace_bytes(0, 5) == 0
 
 
 def test_dense_path_validation(lib):
