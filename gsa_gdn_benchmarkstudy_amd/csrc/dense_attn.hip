@@ -10,22 +10,22 @@
 // key j is selected and valid for query t.
 //
 // Per block: one head, 128 query rows, 4 waves of 32 rows, 64-key tiles
-// staged in LDS.  With v_mfma_f32_32x32x16_bf16 both products are computed
+// in LDS.  With v_mfma_f32_32x32x16_bf16 both products are computed
 // transposed,
 //   S^T = K Q^T    (A = K tile from LDS, B = this wave's q, in registers)
 //   O^T = V^T P^T  (A = V^T tile from LDS, B = P in registers)
 // so in both outputs lane l holds column l%32 = one query row: a query's
 // softmax state lives in its two lanes (l and l^32) and P never moves between
 // lanes.  Accumulator r of lane l is row 8*(r/4) + 4*(l/32) + r%4 of the
-// 32x32 block: keys of S^T, head dims of O^T.
+// 32x32 block: head dims of O^T; the rows of S^T are keys in the permuted
+// order described at the dense kernel.
 #include "gsa_common.h"
 
 namespace gsa {
 
-constexpr int kDQ = 128;         // query rows per block (32 per wave)
+constexpr int kDQ = 128;         // query rows per dense-attention block (32 per wave)
 constexpr int kDK = 64;          // keys per tile
-constexpr int kKS = 128 + 8;     // LDS row stride of the K tile (elements): conflict-free 16-B reads
-constexpr int kVS = kDK + 12;    // LDS row stride of the V^T tile (elements): conflict-free 8-B reads
+constexpr int kKS = 128 + 8;     // LDS row stride of prologue_vt's staging tile (elements)
 
 // ---------------------------------------------------------------------------
 // Producer with transposed V: k_out = RoPE(k) [B,T,H,128], vt = (v*sigmoid(vg))^T
@@ -120,9 +120,9 @@ __global__ __launch_bounds__(256) void selection_mask_kernel(
 // Selection bitmask -> per-lane masks of the dense kernel's score slots.
 // For 32-row group g (rows 32g + i), 64-key tile kt and score slot
 // s = 16c + r (c = 0,1; r = 0..15), lm[b][g][kt][s] bit (32h + i) is the
-// selection bit of row 32g+i and key 64kt + 32c + 8*(r/4) + 4h + r%4 -- the
-// key that accumulator r of lane (h, i) holds in the S^T MFMA output.  One
-// wave per (b, g, kt).
+// selection bit of row 32g+i and key 64kt + 32c + 16(r/8) + 8h + r%8 -- the
+// key that accumulator r of lane (h, i) holds in the S^T MFMA output of half
+// c (see the key order below).  One wave per (b, g, kt).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restrict__ bits, int64_t b_sb,
                                                         int64_t b_st, int T, int G, int NT, int nwaves,
@@ -134,14 +134,14 @@ __global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restri
   const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
   const int row = 32 * g + i;
   uint64_t word = row < T ? *reinterpret_cast<const uint64_t*>(bits + b * b_sb + (int64_t)row * b_st + 2 * kt) : 0ull;
-  word >>= 4 * h;
+  word >>= 8 * h;
   // lane s collects slot s's mask; lanes 0..31 then write 256 contiguous bytes
   uint64_t mine = 0ull;
 #pragma unroll
   for (int c = 0; c < 2; ++c)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const uint64_t m = ballot64((word >> (32 * c + 8 * (r >> 2) + (r & 3))) & 1ull);
+      const uint64_t m = ballot64((word >> (32 * c + 16 * (r >> 3) + (r & 7))) & 1ull);
       mine = lane == 16 * c + r ? m : mine;
     }
   if (lane < 32) lm[((int64_t)bg * NT + kt) * 32 + lane] = mine;
@@ -149,12 +149,32 @@ __global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restri
 
 // ---------------------------------------------------------------------------
 // Dense masked attention (bf16)
+//
+// Block: 4 waves = 128 query rows of one head (wave w: rows 32w .. 32w+31).
+// K and V^T tiles reach LDS by direct global->LDS loads (16 B per lane; one
+// instruction fills 1 KiB, lane-linear), double-buffered, in padded layouts
+// (unit = 16 B = 8 bf16):
+//   K   tile: 64 keys x 17 units, unit 16 of a key is padding
+//   V^T tile: 128 rows x 9 units (64 keys), unit 8 of a row is padding
+// The odd row strides make every MFMA operand read conflict-free (16 lanes
+// reading one unit of 16 different rows hit 16 different bank groups), and
+// each operand read is one base register plus an immediate offset.  Padding
+// units receive a harmless duplicate load.
+// Key order: in the S^T product of a 32-key half, MFMA row rho holds key
+// pi(rho), pi swapping bits 2 and 3 of rho, so accumulator r of lane (h, i)
+// holds key 16(r/8) + 8h + r%8.  A lane's 8 P values of each 16-key k-step
+// are then contiguous keys, and its V^T operand is one 16-byte read.
+//
+// Per tile the two halves are pipelined: S^T of half 1 is computed while the
+// softmax of half 0 runs, and O^T += V^T P^T of half 0 while the softmax of
+// half 1 runs, so MFMA and VALU work of one wave overlap.  Each half is one
+// online-softmax step with the lazy reference (below).
 // ---------------------------------------------------------------------------
 struct DenseArgs {
   const uint16_t* q; int64_t q_sb, q_st;
   const uint16_t* k; int64_t k_sb, k_st;
   const uint16_t* vt; int64_t vt_sb, vt_sh; int ldv;
-  const uint64_t* lm; int G, NT;          // lane masks [B][G][NT][32]
+  int G, NT;                              // lane masks [B][G][NT][32] (kernel argument)
   const uint16_t* og; int64_t o_sb, o_st;
   const uint16_t* cos; const uint16_t* sin; int64_t cs_st;
   uint16_t* out; int64_t out_sb, out_st;
@@ -165,10 +185,27 @@ struct DenseArgs {
 
 constexpr int kDenseCausal = 1 << 8;   // internal flag: skip key tiles after the block's last row
 constexpr float kLazy = 8.f;           // log2 headroom of the lazy softmax reference
+constexpr int kKRow = 17, kVRow = 9;   // padded row lengths in 16-byte units
+constexpr int kKU = kDK * kKRow;       // 1088 units: K tile
+constexpr int kVU = 128 * kVRow;       // 1152 units: V^T tile
+constexpr int kBufU = kKU + kVU;       // one buffer, 35 KiB
+constexpr int kDmaK = kKU / 64;        // 17 load instructions fill a K tile
+constexpr int kDmaV = kVU / 64;        // 18 fill a V^T tile
+constexpr int kDmaWave = 9;            // per wave and tile: instruction 4n + w, wave 3 repeats the last
+constexpr size_t kDenseLds = 2 * kBufU * 16;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+// Value of lane l^32 combined with the own value: permlane32_swap of (v, v)
+// leaves {v[l], v[l^32]} in the two results on every lane.
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // Two fp32 -> packed bf16 (round to nearest even, hardware convert).
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
@@ -176,11 +213,75 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-__global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
-  __shared__ __align__(16) uint16_t sK[kDK * kKS];
-  __shared__ __align__(16) uint16_t sVt[128 * kVS];
+// 32-bit LDS address of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
+}
+
+// Direct global -> LDS load: every lane's 16 bytes at base + voff land at
+// lds + 16 * lane (base and lds uniform).  Issued as inline asm so that the
+// compiler's own bookkeeping does not make each LDS read wait for every such
+// load in flight; completion is awaited explicitly (vmcnt) before the
+// barrier that publishes a tile.  m0 holds the LDS address; nothing else in
+// this kernel uses m0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void load_lds16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Instruction order of the two pipelined regions of a tile (scheduling
+// hints; data dependences still rule).  S region: 16 K operand reads, the 16
+// MFMAs of S^T(half 0) and S^T(half 1), and the softmax of half 0 between
+// the MFMAs of half 1.  PV region: 8 V^T operand reads and the 8 MFMAs of
+// O^T += V^T P^T(half 0), with the softmax of half 1 between them.  Reads
+// run 4 ahead of the MFMAs that use them.
+__device__ __forceinline__ void sched_s_region() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);      // DS reads
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {                            // S^T(half 0)
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // DS read
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {                            // S^T(half 1) || softmax(half 0)
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);   // VALU
+  }
+}
+__device__ __forceinline__ void sched_pv_region() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {                            // O^T += V^T P^T(half 0) || softmax(half 1)
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+  }
+}
+__device__ __forceinline__ void sched_mfma_region() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+}
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt(0), expcnt and lgkmcnt not waited
+constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xf << 8);
+
+__device__ __forceinline__ int swap_bits23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// lm is a separate restrict argument: nothing in this kernel writes it, and
+// alias analysis can see that, so its uniform reads stay scalar loads.
+__global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p, const uint64_t* __restrict__ lm) {
+  extern __shared__ __align__(16) u32x4 dsm[];   // two buffers of kBufU units: K tile, then V^T tile
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
   const int i32 = lane & 31, h = lane >> 5;
   // heaviest query blocks first
   const int nbh = p.B * p.H;
@@ -191,6 +292,58 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
   const int qrow = q0 + 32 * w + i32;
   const int qr = min(qrow, p.T - 1);
 
+  const int last_key = (p.flags & kDenseCausal) ? min(p.Tkv - 1, q0 + kDQ - 1) : p.Tkv - 1;
+  const int nkt = last_key / kDK + 1;
+  const uint16_t* kbase = p.k + b * p.k_sb + hd * 128;
+  const uint16_t* vtb = p.vt + b * p.vt_sb + hd * p.vt_sh;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(dsm));
+
+  // ---- tile loads: wave w issues instructions i = 4n + w (n < 9) ----------
+  // instruction i < 17 fills K units 64i .. 64i+63 (key u/17, unit u%17),
+  // the others V^T units 64(i-17) .. (row u/9, unit u%9): n < 4 are K loads,
+  // n = 4 is K for wave 0 only, n > 4 are V^T loads (wave 3's last repeats
+  // instruction 34).  doff = this lane's source byte offset from the tile's K
+  // or V^T base (32-bit: the host bounds k_st and ldv); doff_last for the
+  // last tile, whose keys past Tkv-1 re-read key Tkv-1.
+  uint32_t doff[kDmaWave], doff_last[5];
+  {
+    const uint32_t kst2 = (uint32_t)p.k_st * 2u, ldv2 = (uint32_t)p.ldv * 2u;
+    const int kmax_last = min(kDK - 1, p.Tkv - 1 - (nkt - 1) * kDK);
+    auto k_off = [&](int i, int kmax) {
+      const int u = i * 64 + lane, key = u / kKRow, c = u - key * kKRow;
+      return (uint32_t)min(key, kmax) * kst2 + (uint32_t)min(c, 15) * 16u;
+    };
+    auto v_off = [&](int iv) {
+      const int u = iv * 64 + lane, d = u / kVRow, c = u - d * kVRow;
+      return (uint32_t)d * ldv2 + (uint32_t)min(c, 7) * 16u;
+    };
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      doff[n] = k_off(4 * n + wu, kDK - 1);
+      doff_last[n] = k_off(4 * n + wu, kmax_last);
+    }
+    doff[4] = wu == 0 ? k_off(16, kDK - 1) : v_off(wu - 1);
+    doff_last[4] = wu == 0 ? k_off(16, kmax_last) : doff[4];
+#pragma unroll
+    for (int n = 5; n < kDmaWave; ++n) doff[n] = v_off(min(4 * n + wu - kDmaK, kDmaV - 1));
+  }
+  auto issue = [&](int kt, int buf) {
+    const int j0 = kt * kDK;
+    const bool last = kt == nkt - 1;
+    const char* kb = reinterpret_cast<const char*>(kbase + (int64_t)j0 * p.k_st);
+    const char* vb = reinterpret_cast<const char*>(vtb + j0);
+    const uint32_t ka = lds0 + (uint32_t)(buf * kBufU * 16);
+    const uint32_t va = ka + kKU * 16;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) load_lds16(kb, last ? doff_last[n] : doff[n], ka + (4 * n + wu) * 1024);
+    if (wu == 0) load_lds16(kb, last ? doff_last[4] : doff[4], ka + 16 * 1024);
+    else load_lds16(vb, doff[4], va + (wu - 1) * 1024);
+#pragma unroll
+    for (int n = 5; n < kDmaWave; ++n) load_lds16(vb, doff[n], va + min(4 * n + wu - kDmaK, kDmaV - 1) * 1024);
+  };
+  issue(0, 0);
+  if (nkt > 1) issue(1, 1);
+
   // ---- q: B operand of S^T; lane supplies d = 16s + 8h .. +7 of its row ----
   u32x4 qraw[8];
   const uint16_t* qp = p.q + b * p.q_sb + (int64_t)qr * p.q_st + hd * 128;
@@ -198,24 +351,29 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
   for (int s = 0; s < 8; ++s) qraw[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * h);
   if (p.flags & GSA_ATTN_ROPE_Q) {
     // rotate_half partner of d (d < 64: -x[d+64]; else x[d-64]) is register s^4
-    float x[8][8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < 4; ++s) {
+      float c0[8], s0[8], c1[8], s1[8];
+      load8(p.cos + (int64_t)qr * p.cs_st + 16 * s + 8 * h, c0);
+      load8(p.sin + (int64_t)qr * p.cs_st + 16 * s + 8 * h, s0);
+      load8(p.cos + (int64_t)qr * p.cs_st + 16 * (s + 4) + 8 * h, c1);
+      load8(p.sin + (int64_t)qr * p.cs_st + 16 * (s + 4) + 8 * h, s1);
+      float lo[8], hi[8], ylo[8], yhi[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { x[s][2 * j] = bf16lo(qraw[s][j]); x[s][2 * j + 1] = bf16hi(qraw[s][j]); }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      float c[8], sn[8], y[8];
-      load8(p.cos + (int64_t)qr * p.cs_st + 16 * s + 8 * h, c);
-      load8(p.sin + (int64_t)qr * p.cs_st + 16 * s + 8 * h, sn);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float a = round_bf16(x[s][j] * c[j]);
-        const float r = round_bf16((s < 4 ? -x[s + 4][j] : x[s - 4][j]) * sn[j]);
-        y[j] = round_bf16(a + r);
+      for (int j = 0; j < 4; ++j) {
+        lo[2 * j] = bf16lo(qraw[s][j]); lo[2 * j + 1] = bf16hi(qraw[s][j]);
+        hi[2 * j] = bf16lo(qraw[s + 4][j]); hi[2 * j + 1] = bf16hi(qraw[s + 4][j]);
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) qraw[s][j] = pack_bf16(y[2 * j], y[2 * j + 1]);
+      for (int j = 0; j < 8; ++j) {
+        ylo[j] = round_bf16(round_bf16(lo[j] * c0[j]) + round_bf16(-hi[j] * s0[j]));
+        yhi[j] = round_bf16(round_bf16(hi[j] * c1[j]) + round_bf16(lo[j] * s1[j]));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qraw[s][j] = pack_bf16(ylo[2 * j], ylo[2 * j + 1]);
+        qraw[s + 4][j] = pack_bf16(yhi[2 * j], yhi[2 * j + 1]);
+      }
     }
   }
   bf16x8 qop[8];
@@ -229,132 +387,113 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
     for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
   float m = -__builtin_inff(), l = 0.f;
 
-  const int last_key = (p.flags & kDenseCausal) ? min(p.Tkv - 1, q0 + kDQ - 1) : p.Tkv - 1;
-  const int nkt = last_key / kDK + 1;
-  const uint16_t* kbase = p.k + b * p.k_sb + hd * 128;
-  const uint16_t* vtb = p.vt + b * p.vt_sb + hd * p.vt_sh;
-  // this wave's lane masks: group 4*qb + w (wave index made uniform for scalar loads)
-  const int wu = __builtin_amdgcn_readfirstlane(w);
-  const uint64_t* lmw = p.lm + ((int64_t)b * p.G + 4 * qb + wu) * p.NT * 32;
+  // this wave's lane masks: group 4*qb + w (wave index uniform for scalar loads)
+  const uint64_t* lmw = lm + ((int64_t)b * p.G + 4 * qb + wu) * p.NT * 32;
+  // operand read bases (units within a buffer): K row of MFMA row i32, V^T row i32
+  const int kread = swap_bits23(i32) * kKRow + h;
+  const int vread = kKU + i32 * kVRow + h;
 
-  // staging: K tile = 64 keys x 16 chunks of 16 B, V^T tile = 128 rows x 8 chunks
-  u32x4 kreg[4], vreg[4];
-  auto fetch = [&](int kt) {
-    const int j0 = kt * kDK;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int item = it * 256 + tid;
-      const int key = item >> 4, c = item & 15;
-      const int j = j0 + key;
-      kreg[it] = j < p.Tkv ? *reinterpret_cast<const u32x4*>(kbase + (int64_t)j * p.k_st + c * 8)
-                           : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int item = it * 256 + tid;
-      const int d = item >> 3, c8 = item & 7;
-      vreg[it] = *reinterpret_cast<const u32x4*>(vtb + (int64_t)d * p.ldv + j0 + 8 * c8);
-    }
-  };
-  auto stash = [&]() {
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int item = it * 256 + tid;
-      const int key = item >> 4, c = item & 15;
-      *reinterpret_cast<u32x4*>(sK + key * kKS + c * 8) = kreg[it];
-    }
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int item = it * 256 + tid;
-      const int d = item >> 3, c8 = item & 7;
-      uint2* dst = reinterpret_cast<uint2*>(sVt + d * kVS + 8 * c8);
-      dst[0] = uint2{vreg[it][0], vreg[it][1]};
-      dst[1] = uint2{vreg[it][2], vreg[it][3]};
-    }
-  };
+  // The q (and cos/sin) loads have landed.  The wait is the compiler's own
+  // intrinsic, so it knows that none of its loads is still in flight and puts
+  // no vmcnt wait into the loop, where the counter also counts the tile loads
+  // and any such wait would drain them.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
-  fetch(0);
   for (int kt = 0; kt < nkt; ++kt) {
-    __syncthreads();   // the previous tile's LDS reads are done
-    stash();
-    __syncthreads();
-    if (kt + 1 < nkt) fetch(kt + 1);   // next tile's loads fly during this tile's math
+    const int buf = kt & 1;
+    // this wave's loads of tile kt are done (tile kt+1's may still fly); the
+    // barrier publishes every wave's part
+    if (kt + 1 < nkt) asm volatile("s_waitcnt vmcnt(9)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    const u32x4* sK = dsm + buf * kBufU + kread;
+    const u32x4* sV = dsm + buf * kBufU + vread;
+    const uint64_t* lmt = lmw + kt * 32;
 
-    const uint64_t* lmt = lmw + kt * 32;   // 32 slot masks of this tile
-
-    // ---- S^T = K Q^T: two 32-key subtiles ----
-    floatx16 sacc[2];
+    auto s_half = [&](int c) {
+      bf16x8 f[8];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+      for (int s = 0; s < 8; ++s) f[s] = __builtin_bit_cast(bf16x8, sK[32 * c * kKRow + 2 * s]);
       floatx16 acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(sK + (32 * c + i32) * kKS + 16 * s + 8 * h);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qop[s], acc, 0, 0, 0);
-      }
-      sacc[c] = acc;
-    }
-
-    // ---- masked online softmax (log2 domain, lazy reference max) ----
-    // p = 2^(s*scale*log2e - m) against a per-row reference m that only moves
-    // when the row max exceeds it by more than kLazy: p <= 2^kLazy, so O and l
-    // are rescaled rarely; out = O / l does not depend on m.
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
+      for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[s], qop[s], acc, 0, 0, 0);
+      return acc;
+    };
+    // masked online-softmax step over one half: p = 2^(s*scale*log2e - m)
+    // against a per-row reference m that only moves when the row max exceeds
+    // it by more than kLazy (p <= 2^kLazy; O and l are rescaled rarely; out =
+    // O / l does not depend on m).  Returns P as two B operands of O^T.
+    auto softmax_half = [&](const floatx16& acc, int c, uint32_t (&pk)[2][4], float& alpha) -> bool {
+      float sv[16];
+      float mx = -__builtin_inff();
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const bool sel = __builtin_amdgcn_inverse_ballot_w64(lmt[16 * c + r]);
-        sacc[c][r] = sel ? sacc[c][r] : -__builtin_inff();
-        mx = fmaxf(mx, sacc[c][r]);
+        sv[r] = sel ? acc[r] : -__builtin_inff();
+        mx = fmaxf(mx, sv[r]);
       }
-    mx = fmaxf(mx, xor32(mx)) * p.scale_l2;
-    const bool bump = mx > m + kLazy || (m == -__builtin_inff() && mx != -__builtin_inff());
-    const float mref = bump ? mx : m;
-    const float alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
-    const float msafe = mref == -__builtin_inff() ? 0.f : mref;
-    // P as the B operand of O^T: k-step ks = 2c + s2 covers keys
-    // 32c + 16*s2 + 4h + {0..3} and 32c + 16*s2 + 8 + 4h + {0..3}
-    uint32_t pk[4][4];
-    float lsum = 0.f;
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
+      mx = max_halves(mx) * p.scale_l2;
+      const bool bump = mx > m + kLazy || (m == -__builtin_inff() && mx != -__builtin_inff());
+      const float mref = bump ? mx : m;
+      alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
+      const float msafe = mref == -__builtin_inff() ? 0.f : mref;
+      float lsum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[c][r], p.scale_l2, -msafe));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[c][r + 1], p.scale_l2, -msafe));
-        pk[2 * c + (r >> 3)][(r & 7) >> 1] = cvt_pk_bf16(p0, p1);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], p.scale_l2, -msafe));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r + 1], p.scale_l2, -msafe));
+        pk[r >> 3][(r & 7) >> 1] = cvt_pk_bf16(p0, p1);
         lsum += p0 + p1;
       }
-    l = l * alpha + lsum;
-    if (ballot64(bump)) {
+      l = l * alpha + lsum;
+      m = mref;
+      return bump;
+    };
+    auto rescale = [&](float alpha) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-    }
-    m = mref;
-
-    // ---- O^T += V^T P^T ----
+    };
+    auto pv_half = [&](int c, const uint32_t (&pk)[2][4]) {
+      bf16x8 f[2][4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pk[ks][0], pk[ks][1], pk[ks][2], pk[ks][3]});
-      const int koff = 32 * (ks >> 1) + 16 * (ks & 1) + 4 * h;
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const uint16_t* vr = sVt + (32 * dt + i32) * kVS + koff;
-        const uint2 a0 = *reinterpret_cast<const uint2*>(vr);
-        const uint2 a1 = *reinterpret_cast<const uint2*>(vr + 8);
-        const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{a0.x, a0.y, a1.x, a1.y});
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[dt], 0, 0, 0);
+        for (int dt = 0; dt < 4; ++dt)
+          f[ks][dt] = __builtin_bit_cast(bf16x8, sV[32 * dt * kVRow + 4 * c + 2 * ks]);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pk[ks][0], pk[ks][1], pk[ks][2], pk[ks][3]});
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[ks][dt], pb, o[dt], 0, 0, 0);
       }
+    };
+
+    uint32_t pk0[2][4], pk1[2][4];
+    float alpha0, alpha1;
+    const floatx16 s0 = s_half(0);
+    const floatx16 s1 = s_half(1);                 // overlaps the softmax of half 0
+    const bool bump0 = softmax_half(s0, 0, pk0, alpha0);
+    sched_s_region();
+    if (ballot64(bump0)) rescale(alpha0);
+    pv_half(0, pk0);                               // overlaps the softmax of half 1
+    const bool bump1 = softmax_half(s1, 1, pk1, alpha1);
+    sched_pv_region();
+    if (ballot64(bump1)) rescale(alpha1);
+    pv_half(1, pk1);
+    sched_mfma_region();
+
+    // every wave is done reading this buffer before it is refilled
+    if (kt + 2 < nkt) {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue(kt + 2, buf);
     }
   }
 
   // ---- epilogue: normalise, bf16, optional output gate ----
-  l += xor32(l);
+  l = sum_halves(l);
   if (qrow < p.T) {
     uint16_t* op = p.out + b * p.out_sb + (int64_t)qrow * p.out_st + hd * 128;
     const uint16_t* gp = (p.flags & GSA_ATTN_OUT_GATE) ? p.og + b * p.o_sb + (int64_t)qrow * p.o_st + hd * 128
@@ -384,6 +523,11 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p) {
 // Host entry points
 // ---------------------------------------------------------------------------
 using namespace gsa_host;
+
+// Per device: the dense kernel's LDS limit has been raised.  (A benign race:
+// concurrent first calls both set the same attribute.)
+static constexpr int kMaxDevices = 64;
+static bool g_dense_lds_set[kMaxDevices] = {};
 
 extern "C" int gsa_prologue_vt(const void* k, int64_t k_sb, int64_t k_st,
                                const void* v, int64_t v_sb, int64_t v_st,
@@ -428,9 +572,12 @@ extern "C" int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st
   return launch_status();
 }
 
+// Lane masks: 32 per (batch, 32-row group, 64-key tile); the groups are
+// counted over whole 128-row query blocks.
 extern "C" size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv) {
   if (B < 1 || T < 1 || Tkv < 1) return 0;
-  return (size_t)B * ((T + 31) / 32) * ((Tkv + 63) / 64) * 32 * sizeof(uint64_t);
+  const size_t groups = (size_t)((T + gsa::kDQ - 1) / gsa::kDQ) * (gsa::kDQ / 32);
+  return (size_t)B * groups * ((Tkv + 63) / 64) * 32 * sizeof(uint64_t);
 }
 
 extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
@@ -454,6 +601,8 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   if (ldv < NT * 64 || ldv % 64 != 0) return GSA_ERR_SHAPE;
   if (b_st < 2 * NT || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
   if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
+  // per-lane load offsets within a tile are 32-bit byte offsets
+  if (k_st > (1 << 24) || (int64_t)ldv > (1 << 23)) return GSA_ERR_SHAPE;
   const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
   const int G = nqb * (gsa::kDQ / 32);    // 32-row groups, padded to whole blocks
   if ((int64_t)B * H * nqb > 0x7fffffffLL || (int64_t)B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
@@ -471,10 +620,19 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   int st = launch_status();
   if (st) return st;
   gsa::DenseArgs a{static_cast<const uint16_t*>(q), q_sb, q_st, static_cast<const uint16_t*>(k), k_sb, k_st,
-                   static_cast<const uint16_t*>(vt), vt_sb, vt_sh, ldv, lm, G, NT,
+                   static_cast<const uint16_t*>(vt), vt_sb, vt_sh, ldv, G, NT,
                    static_cast<const uint16_t*>(og), o_sb, o_st, static_cast<const uint16_t*>(cos),
                    static_cast<const uint16_t*>(sin), cs_st, static_cast<uint16_t*>(out), out_sb, out_st,
                    B, T, Tkv, H, nqb, scale * gsa::kLog2e, flags | (causal ? gsa::kDenseCausal : 0)};
-  hipLaunchKernelGGL(gsa::dense_attn_kernel, dim3(B * H * nqb), dim3(256), 0, s, a);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return GSA_ERR_SHAPE;
+  if (!g_dense_lds_set[dev]) {   // more than the default 64 KiB of LDS per block
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gsa::dense_attn_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsa::kDenseLds);
+    if (e != hipSuccess) return -static_cast<int>(e);
+    g_dense_lds_set[dev] = true;
+  }
+  hipLaunchKernelGGL(gsa::dense_attn_kernel, dim3(B * H * nqb), dim3(256), gsa::kDenseLds, s, a,
+                     static_cast<const uint64_t*>(lm));
   return launch_status();
 }
