@@ -204,13 +204,34 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 // starting at tile b*tri(G) + tri(g), tri(n) = n(n+1)/2, G = ceil(T/16);
 // lane l of the wave that computes a tile stores its four output slots
 // (rows 4*(l/16)+e, column l%16) as floats 4l .. 4l+3, the layout it reads
-// back.
+// back.  After the score tiles, block i owns 16 x kCap (key, index) slots
+// for its rows' candidates (kept out of LDS, so that a block needs only its
+// 17 KiB of histograms and can share a CU with a GEMM block).
 // ---------------------------------------------------------------------------
 constexpr int kNB = 512;                 // histogram bins per row
 constexpr int kCap = 512;                // candidates per row
-constexpr int kHStride = kNB + 1;        // odd stride: one bin of 16 rows in distinct banks
 constexpr int kGroupWaves = 4;
 constexpr int kWCap = kCap / kGroupWaves;  // candidates per row and wave
+
+// Per-row histogram in LDS.  Packed: 512 bins as 16-bit counts, two per
+// word (exact while a row has at most 65535 keys, i.e. T <= 65535), 17 KiB
+// for the block -- small enough for a block to share a CU with the
+// projection GEMM's.  Unpacked: 32-bit counts.  Bin kNB is a trash bin
+// (invalid slots) in the row's padding word, which no scan reads; the odd
+// row strides put one bin of the 16 rows in distinct banks.  The overflow
+// path's 256-bin digit histograms use 32-bit words with either stride.
+template <bool kPacked>
+struct Hist {
+  static constexpr int kStride = kPacked ? kNB / 2 + 1 : kNB + 1;
+  __device__ static void add(uint32_t* row, int bin) {
+    if constexpr (kPacked) atomicAdd(&row[bin >> 1], 1u << (16 * (bin & 1)));
+    else atomicAdd(&row[bin], 1u);
+  }
+  __device__ static int count(const uint32_t* row, int bin) {
+    if constexpr (kPacked) return (int)((row[bin >> 1] >> (16 * (bin & 1))) & 0xffffu);
+    else return (int)row[bin];
+  }
+};
 constexpr int kTile = 256;               // floats per stored 16x16 score tile
 
 enum RowMode : int { kNone = 0, kTrivial = 1, kActive = 2, kResolved = 3, kOverflow = 4 };
@@ -225,11 +246,12 @@ __device__ __forceinline__ uint16_t prefix_chunk(int row, int tile) {
   return n >= 16 ? (uint16_t)0xffffu : (n <= 0 ? (uint16_t)0 : (uint16_t)((1u << n) - 1u));
 }
 
-template <typename T>
+template <typename T, bool kPacked>
 __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff, uint32_t* bits,
-                                                           int64_t b_sb, int64_t b_st, float* ws) {
-  __shared__ uint32_t sh[16 * kHStride];   // histogram, then candidate keys
-  __shared__ uint32_t sh_idx[16 * kCap];   // candidate key indices
+                                                           int64_t b_sb, int64_t b_st, float* ws, uint2* ws_cand) {
+  using H = Hist<kPacked>;
+  constexpr int kHStride = H::kStride;
+  __shared__ uint32_t sh[16 * kHStride];   // histograms
   __shared__ uint32_t sh_wcnt[16 * kGroupWaves];
   __shared__ int st_mode[16], st_b1[16], st_need[16];
   __shared__ uint32_t st_key[16];
@@ -245,6 +267,8 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
   uint16_t* b16 = reinterpret_cast<uint16_t*>(bbase);
   const int64_t row16 = 2 * b_st;          // uint16 chunks per row
   float* wsg = ws + ((int64_t)b * ngroups * (ngroups + 1) / 2 + (int64_t)rg_idx * (rg_idx + 1) / 2) * kTile;
+  // this block's candidates (key, index): row rl, wave w, slot i at [rl][w * kWCap + i]
+  uint2* cand = ws_cand + (int64_t)blockIdx.x * 16 * kCap;
 
   if (tid < 16) {
     const int row = r0 + tid;
@@ -306,7 +330,7 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
   auto scan_row = [&](int rl, int& nd) -> int {     // top-down cumulative search
     int cum = 0, bsel = 0;
     for (int bin = kNB - 1; bin >= 0; --bin) {
-      const int c = (int)sh[rl * kHStride + bin];
+      const int c = H::count(&sh[rl * kHStride], bin);
       if (cum + c >= nd) { bsel = bin; break; }
       cum += c;
     }
@@ -336,7 +360,7 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
       for (int e = 0; e < 4; ++e) {
         sc[e] = rgp.score(acc, e);
         const int bn = valid[e] ? bin_of(sc[e], inv_w[e]) : kNB;
-        atomicAdd(&sh[(4 * g + e) * kHStride + bn], 1u);
+        H::add(&sh[(4 * g + e) * kHStride], bn);
       }
       *reinterpret_cast<floatx4*>(wsg + t * kTile + lane * 4) = sc;
     }
@@ -350,7 +374,6 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
   __syncthreads();
 #pragma unroll
   for (int e = 0; e < 4; ++e) b1[e] = st_b1[4 * g + e];
-  __syncthreads();   // sh is reused for candidate keys below
 
   // Replay of the stored tiles in quads of 4 consecutive tiles (quad j =
   // tiles 4j .. 4j+3, one 64-key word pair of the mask).  Each wave takes
@@ -395,7 +418,8 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
 
   // ---- pass 2: bins above b1 -> mask words; bin b1 -> candidates -------------
   // Candidates of row 4g+e found by this wave go to its own region of the
-  // row (kWCap slots), positions from a per-wave count: no atomics.  Lane
+  // row's list in the workspace (kWCap slots), positions from a per-wave
+  // count: no atomics.  Lane
   // 16g+e assembles row 4g+e's 64-bit mask word of each quad.
   int wc[4] = {0, 0, 0, 0};
   const uint32_t below = (1u << lr) - 1u;
@@ -407,16 +431,13 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
         for (int e = 0; e < 4; ++e) {
           const int bn = bin_of(sc[e], inv_w[e]);
           m[e] = ballot64(valid[e] && bn > b1[e]);
-          const bool cand = valid[e] && bn == b1[e];
-          const uint64_t cm = ballot64(cand);
+          const bool is_cand = valid[e] && bn == b1[e];
+          const uint64_t cm = ballot64(is_cand);
           if (cm) {
             const uint32_t gm = (uint32_t)(cm >> (16 * g)) & 0xffffu;
             const int pos = wc[e] + __popc(gm & below);
-            if (cand && pos < kWCap) {
-              const int rl = 4 * g + e;
-              sh[rl * kHStride + wave * kWCap + pos] = score_key(sc[e]);
-              sh_idx[rl * kCap + wave * kWCap + pos] = (uint32_t)col;
-            }
+            if (is_cand && pos < kWCap)
+              cand[(4 * g + e) * kCap + wave * kWCap + pos] = uint2{score_key(sc[e]), (uint32_t)col};
             wc[e] += __popc(gm);
           }
         }
@@ -431,9 +452,10 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
 #pragma unroll
     for (int e = 0; e < 4; ++e) sh_wcnt[(4 * g + e) * kGroupWaves + wave] = (uint32_t)wc[e];
   }
-  // The resolve's atomics below come from waves of this block only: the
-  // barrier (a workgroup-scope release/acquire) orders the mask stores above
-  // before them.  A device-scope fence here would write back the whole L2.
+  // The resolve's atomics and candidate reads below come from waves of this
+  // block only: the barrier (a workgroup-scope release/acquire) orders the
+  // mask and candidate stores above before them.  A device-scope fence here
+  // would write back the whole L2.
   __syncthreads();
 
   // ---- resolve: wave w takes rows 4w .. 4w+3 ----------------------------------
@@ -461,8 +483,9 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
       const int w = i >> 1, pos = (i & 1) * 64 + lane;
       used[i] = (i & 1) * 64 < nw[w];
       cvalid[i] = pos < nw[w];
-      cv[i] = cvalid[i] ? sh[rl * kHStride + w * kWCap + pos] : 0u;
-      ci[i] = cvalid[i] ? sh_idx[rl * kCap + w * kWCap + pos] : 0u;
+      const uint2 cd = cvalid[i] ? cand[rl * kCap + w * kWCap + pos] : uint2{0u, 0u};
+      cv[i] = cd.x;
+      ci[i] = cd.y;
       if (cvalid[i]) { kor |= cv[i]; kand &= cv[i]; }
     }
     // Bits on which every candidate agrees are part of theta; the radix
@@ -504,9 +527,10 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
         } else {
           int rank = 0;
           for (int w = 0; w < kGroupWaves; ++w)
-            for (int o = 0; o < nw[w]; ++o)
-              rank += (sh[rl * kHStride + w * kWCap + o] == prefix &&
-                       sh_idx[rl * kCap + w * kWCap + o] < ci[i]) ? 1 : 0;
+            for (int o = 0; o < nw[w]; ++o) {
+              const uint2 cd = cand[rl * kCap + w * kWCap + o];
+              rank += (cd.x == prefix && cd.y < ci[i]) ? 1 : 0;
+            }
           win = rank < k;
         }
       }
@@ -687,10 +711,17 @@ extern "C" int gsa_indexer_scores(const void* q_idx, int64_t q_sb, int64_t q_st,
   return launch_status();
 }
 
+// Score tiles (1 KiB per causal 16x16 tile), then the candidate lists
+// (16 rows x kCap (key, index) pairs per 16-row group).
+static size_t score_ws_bytes(int B, int T) {
+  const size_t g = (size_t)((T + 15) / 16);
+  return (size_t)B * (g * (g + 1) / 2) * gsa::kTile * sizeof(float);
+}
+
 extern "C" size_t gsa_indexer_select_workspace_bytes(int B, int T) {
   if (B < 1 || T < 1) return 0;
   const size_t g = (size_t)((T + 15) / 16);
-  return (size_t)B * (g * (g + 1) / 2) * gsa::kTile * sizeof(float);
+  return score_ws_bytes(B, T) + (size_t)B * g * 16 * gsa::kCap * sizeof(uint2);
 }
 
 extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
@@ -716,12 +747,21 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
   gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
   const int ngroups = (T + 15) / 16;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == GSA_DTYPE_BF16)
-    hipLaunchKernelGGL(gsa::indexer_bits_kernel<uint16_t>, dim3(B * ngroups), dim3(256), 0, s, a, k_eff, bits,
-                       b_sb, b_st, static_cast<float*>(ws));
-  else
-    hipLaunchKernelGGL(gsa::indexer_bits_kernel<float>, dim3(B * ngroups), dim3(256), 0, s, a, k_eff, bits,
-                       b_sb, b_st, static_cast<float*>(ws));
+  float* wsf = static_cast<float*>(ws);
+  uint2* wsc = reinterpret_cast<uint2*>(static_cast<char*>(ws) + score_ws_bytes(B, T));
+  const bool packed = T <= 65535;   // 16-bit histogram counts are exact
+  const dim3 grid(B * ngroups), block(256);
+  if (dtype == GSA_DTYPE_BF16) {
+    if (packed)
+      hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, true>), grid, block, 0, s, a, k_eff, bits, b_sb, b_st, wsf, wsc);
+    else
+      hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, false>), grid, block, 0, s, a, k_eff, bits, b_sb, b_st, wsf, wsc);
+  } else {
+    if (packed)
+      hipLaunchKernelGGL((gsa::indexer_bits_kernel<float, true>), grid, block, 0, s, a, k_eff, bits, b_sb, b_st, wsf, wsc);
+    else
+      hipLaunchKernelGGL((gsa::indexer_bits_kernel<float, false>), grid, block, 0, s, a, k_eff, bits, b_sb, b_st, wsf, wsc);
+  }
   st = launch_status();
   if (st || !idx_out) return st;
   hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_eff,

@@ -112,7 +112,8 @@ int gsa_topk_select(const float* scores, int64_t s_sb, int64_t s_st,
  * ws: caller-provided device workspace of at least
  * gsa_indexer_select_workspace_bytes(B, T) bytes (16-byte aligned),
  * overwritten by each call: the causal score tiles, stored once and read
- * back instead of recomputed (B * G(G+1)/2 KiB, G = ceil(T/16)).
+ * back instead of recomputed (B * G(G+1)/2 KiB, G = ceil(T/16)), and the
+ * threshold candidates of each 16-row group (B * G * 64 KiB).
  * Supported: Hi == 4, di == 64, 1 <= k_eff <= T.
  */
 size_t gsa_indexer_select_workspace_bytes(int B, int T);

@@ -76,9 +76,12 @@ def test_indexer_scores_validation(lib):
     assert _scores(lib, qst=260) == 4        # row stride not a multiple of 8 bf16
 
 
+NWS_T32 = 3 * 1024 + 2 * 16 * 512 * 8    # indexer-select workspace at B=1, T=32
+
+
 def _select(lib, **kw):
     a = dict(q=P, qsb=0, qst=256, k=P, ksb=0, kst=64, w=P, wsb=0, wst=4, bias=P, scale=0.125,
-             B=1, T=32, Hi=4, di=64, k_eff=8, dtype=1, bits=P, bsb=0, bst=2, idx=P, cnt=P, ws=P, nws=3072)
+             B=1, T=32, Hi=4, di=64, k_eff=8, dtype=1, bits=P, bsb=0, bst=2, idx=P, cnt=P, ws=P, nws=NWS_T32)
     a.update(kw)
     return lib.gsa_indexer_select(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["w"], a["wsb"],
                                   a["wst"], a["bias"], a["scale"], a["B"], a["T"], a["Hi"], a["di"],
@@ -97,12 +100,14 @@ def test_indexer_select_validation(lib):
     assert _select(lib, bst=1) == 2               # fewer words than 2*ceil(T/64)
     assert _select(lib, bits=P + 4) == 4          # rows must be 8-byte aligned
     assert _select(lib, ws=None) == 1
-    assert _select(lib, nws=3071) == 2            # score workspace too small
+    assert _select(lib, nws=NWS_T32 - 1) == 2     # workspace too small
     assert _select(lib, ws=P + 8) == 4
-    # one 1 KiB tile per causal (16-row group, 16-key tile) pair
-    assert lib.gsa_indexer_select_workspace_bytes(1, 32) == 3 * 1024
-    assert lib.gsa_indexer_select_workspace_bytes(2, 100) == 2 * 28 * 1024
-    assert lib.gsa_indexer_select_workspace_bytes(1, 65536) == 4096 * 4097 // 2 * 1024
+    # one 1 KiB score tile per causal (16-row group, 16-key tile) pair, then
+    # 16 rows x 512 (key, index) candidate slots of 8 bytes per 16-row group
+    cand = 16 * 512 * 8
+    assert lib.gsa_indexer_select_workspace_bytes(1, 32) == NWS_T32 == 3 * 1024 + 2 * cand
+    assert lib.gsa_indexer_select_workspace_bytes(2, 100) == 2 * (28 * 1024 + 7 * cand)
+    assert lib.gsa_indexer_select_workspace_bytes(1, 65536) == 4096 * 4097 // 2 * 1024 + 4096 * cand
     assert lib.gsa_indexer_select_workspace_bytes(0, 5) == 0
 
 
