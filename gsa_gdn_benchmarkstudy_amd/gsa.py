@@ -130,10 +130,19 @@ class RotaryEmbedding(nn.Module):
                 dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
         if seq_len > self.cos_cached.shape[0]:
             self._build_cache(seq_len, self.inv_freq)
+        # The cast tables are kept while the cache they came from is unchanged
+        # (same storage and version): casting again would give the same values.
+        key = (self.cos_cached.data_ptr(), self.cos_cached._version, self.sin_cached.data_ptr(),
+               self.sin_cached._version, seq_len, torch.device(device), dtype)
+        hit = getattr(self, "_cast", None)
+        if hit is not None and hit[0] == key:
+            return hit[1], hit[2]
         cos = self.cos_cached[:seq_len].to(device)
         sin = self.sin_cached[:seq_len].to(device)
         if dtype is not None:
             cos, sin = cos.to(dtype), sin.to(dtype)
+        cos, sin = cos.contiguous(), sin.contiguous()
+        self._cast = (key, cos, sin)
         return cos, sin
 
 
