@@ -165,6 +165,7 @@ def main():
         for _ in range(args.warmup):
             model(x)
         torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
         model.attn_events = []
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
@@ -175,6 +176,7 @@ def main():
         evs = model.attn_events
         model.attn_events = None
     total_ms = start.elapsed_time(end)
+    peak_mem = torch.cuda.max_memory_allocated(dev)     # during the timed forwards
     ms = total_ms / args.steps
     attn_impl = "dense" if model.uses_dense(dtype) else "gather"
     attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
@@ -263,7 +265,9 @@ def main():
         "gather_attention": gather_roof,
         "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,
                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": idx_tflops / BF16_PEAK_TFLOPS,
+                    "traffic": profiled_traffic("gsa_indexer_select", args.config),
                     "flops": fidx, "ms": idx_ms},
+        "peak_mem_gib": peak_mem / 2**30,
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, T, args.cpu_seconds)
