@@ -34,7 +34,8 @@ EXPORTS = (
     "gsa_abi_version", "gsa_status_string", "gsa_indexer_scores", "gsa_topk_select",
     "gsa_indexer_select", "gsa_prologue", "gsa_sparse_attn", "gsa_prologue_vt",
     "gsa_selection_mask", "gsa_dense_attn", "gsa_dense_attn_workspace_bytes",
-    "gsa_indexer_select_workspace_bytes",
+    "gsa_indexer_select_workspace_bytes", "gsa_indexer_select_adaptive",
+    "gsa_indexer_select_adaptive_workspace_bytes", "gsa_topk_select_adaptive",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -45,10 +46,17 @@ _PROTOS = {
     "gsa_indexer_scores": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
                             _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp], _i32),
     "gsa_topk_select": ([_vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
+    "gsa_topk_select_adaptive": ([_vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                  _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "gsa_indexer_select": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
                             _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp,
                             _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_indexer_select_workspace_bytes": ([_i32, _i32], ctypes.c_size_t),
+    "gsa_indexer_select_adaptive": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
+                                     _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                     _vp, _i64, _i64, _vp, _vp, _vp, _vp,
+                                     _vp, ctypes.c_size_t, _vp], _i32),
+    "gsa_indexer_select_adaptive_workspace_bytes": ([_i32, _i32], ctypes.c_size_t),
     "gsa_prologue": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
                       _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
     "gsa_sparse_attn": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
@@ -179,6 +187,33 @@ def topk_select(scores: torch.Tensor, k_eff: int, order: int = ORDER_INDEX_ASC,
     return idx, cnt, mask
 
 
+def topk_select_adaptive(scores: torch.Tensor, k_base: int, k_min: int, k_max: int,
+                         order: int = ORDER_INDEX_ASC, want_mask: bool = False):
+    """Per-row top-k with the variance-based k of fp32 scores [B,T,Tkv] ->
+    (idx int32 [B,T,W], count int32 [B,T], mask uint8|None, k int32 [B,T],
+    var fp32 [B,T]), W = min(k_max, Tkv)."""
+    lib = load()
+    _need_cuda(scores)
+    if scores.dtype != torch.float32:
+        raise TypeError("scores must be float32")
+    _expect(scores.dim() == 3, "scores: [B,T,Tkv]")
+    B, T, Tkv = scores.shape
+    if scores.stride(2) != 1:
+        raise ValueError("scores must have unit column stride")
+    W = min(int(k_max), Tkv)
+    dev = scores.device
+    idx = torch.empty(B, T, W, device=dev, dtype=torch.int32)
+    cnt = torch.empty(B, T, device=dev, dtype=torch.int32)
+    mask = torch.empty(B, T, W, device=dev, dtype=torch.uint8) if want_mask else None
+    k_rows = torch.empty(B, T, device=dev, dtype=torch.int32)
+    var = torch.empty(B, T, device=dev, dtype=torch.float32)
+    st = lib.gsa_topk_select_adaptive(_ptr(scores), scores.stride(0), scores.stride(1), B, T, Tkv,
+                                      int(k_base), int(k_min), int(k_max), int(order), _ptr(idx),
+                                      _ptr(cnt), _ptr(mask), _ptr(k_rows), _ptr(var), _stream(scores))
+    _check(st, "gsa_topk_select_adaptive")
+    return idx, cnt, mask, k_rows, var
+
+
 def indexer_select_workspace_bytes(B: int, T: int) -> int:
     return int(load().gsa_indexer_select_workspace_bytes(B, T))
 
@@ -218,6 +253,52 @@ def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int, indices: b
                                 _ptr(ws), nbytes, _stream(q_idx))
     _check(st, "gsa_indexer_select")
     return bits, idx, cnt
+
+
+def indexer_select_adaptive_workspace_bytes(B: int, T: int) -> int:
+    return int(load().gsa_indexer_select_adaptive_workspace_bytes(B, T))
+
+
+def indexer_select_adaptive(q_idx, k_idx, w, bias32, scale: float, k_base: int, k_min: int,
+                            k_max: int, indices: bool = True, bits: Optional[torch.Tensor] = None,
+                            ws: Optional[torch.Tensor] = None):
+    """Fused indexer + exact top-k with the variance-based per-row k.
+
+    Returns (bits, idx, count, k_rows, var): the selection bitmask int32
+    [B,T,W]; when ``indices``, ascending int32 indices [B,T,min(k_max,T)] and
+    counts int32 [B,T] (else None, None); the per-row k int32 [B,T] and the
+    per-row score variance fp32 [B,T].
+    """
+    lib = load()
+    _need_cuda(q_idx, k_idx, w, bias32)
+    B, T, Hi, di = q_idx.shape
+    _expect(tuple(k_idx.shape) == (B, T, di), f"k_idx {tuple(k_idx.shape)} != {(B, T, di)}")
+    _expect(tuple(w.shape) == (B, T, Hi), f"w {tuple(w.shape)} != {(B, T, Hi)}")
+    _expect(bias32.dtype == torch.float32 and bias32.numel() == Hi and bias32.is_contiguous(), "bias: fp32 [Hi]")
+    _expect(k_idx.dtype == q_idx.dtype == w.dtype, "q_idx, k_idx, w must share a dtype")
+    dev = q_idx.device
+    W = mask_words(T)
+    if bits is None:
+        bits = torch.empty(B, T, W, device=dev, dtype=torch.int32)
+    _expect(tuple(bits.shape) == (B, T, W) and bits.is_contiguous(), "bits: contiguous [B,T,W]")
+    idx = cnt = None
+    if indices:
+        idx = torch.empty(B, T, min(int(k_max), T), device=dev, dtype=torch.int32)
+        cnt = torch.empty(B, T, device=dev, dtype=torch.int32)
+    k_rows = torch.empty(B, T, device=dev, dtype=torch.int32)
+    var = torch.empty(B, T, device=dev, dtype=torch.float32)
+    nbytes = lib.gsa_indexer_select_adaptive_workspace_bytes(B, T)
+    if ws is None:
+        ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    _expect(ws.numel() * ws.element_size() >= nbytes and ws.is_contiguous(), "workspace too small")
+    qs, ks, wst = _rows(q_idx, Hi * di), _rows(k_idx, di), _rows(w, Hi)
+    st = lib.gsa_indexer_select_adaptive(
+        _ptr(q_idx), *qs, _ptr(k_idx), *ks, _ptr(w), *wst, _ptr(bias32), float(scale), B, T, Hi, di,
+        int(k_base), int(k_min), int(k_max), dtype_code(q_idx.dtype),
+        _ptr(bits), bits.stride(0), bits.stride(1), _ptr(idx), _ptr(cnt), _ptr(k_rows), _ptr(var),
+        _ptr(ws), nbytes, _stream(q_idx))
+    _check(st, "gsa_indexer_select_adaptive")
+    return bits, idx, cnt, k_rows, var
 
 
 def prologue(k=None, v=None, vg=None, cos=None, sin=None, k_out=None, v_out=None):

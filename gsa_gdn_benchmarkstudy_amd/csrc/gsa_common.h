@@ -169,4 +169,10 @@ inline int launch_status() {
   return e == hipSuccess ? GSA_OK : -static_cast<int>(e);
 }
 
+// Variance-based per-row k from per-row variances var[0..n) (indexer.hip):
+// k = min(clamp(floor(k_base * max(mean(var),1e-6) / max(var,1e-6)), k_min, k_max), k_cap).
+// One launch on `stream`; returns launch_status().
+int launch_adaptive_k(const float* var, int n, int k_base, int k_min, int k_max, int k_cap, int32_t* k_rows,
+                      hipStream_t stream);
+
 }  // namespace gsa_host

@@ -246,8 +246,25 @@ __device__ __forceinline__ uint16_t prefix_chunk(int row, int tile) {
   return n >= 16 ? (uint16_t)0xffffu : (n <= 0 ? (uint16_t)0 : (uint16_t)((1u << n) - 1u));
 }
 
-template <typename T, bool kPacked>
-__global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff, uint32_t* bits,
+// Selection parameters of one launch.  The kernel runs in one of three phases:
+//   0  fused: every row takes k = k_eff (the reference selector);
+//   1  variance-adaptive k, first launch: pass 1 only, then each row's
+//      population variance of its causal scores -> row_var, and the block's
+//      histograms -> hist (scores stay in the workspace);
+//   2  variance-adaptive k, second launch: row t takes k = k_rows[b*T+t]; the
+//      histograms come back from hist instead of pass 1, then pass 2,
+//      resolve and overflow as in phase 0.
+// k_rows is written between the two launches by adaptive_k_kernel, which
+// needs every row's variance (its mean over all rows is global).
+struct SelArgs {
+  int k_eff;              // phase 0
+  const int* k_rows;      // phase 2: [B*T]
+  float* row_var;         // phase 1: [B*T]
+  uint32_t* hist;         // phases 1, 2: 16 * Hist::kStride words per block
+};
+
+template <typename T, bool kPacked, int kPhase>
+__global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, SelArgs sa, uint32_t* bits,
                                                            int64_t b_sb, int64_t b_st, float* ws, uint2* ws_cand) {
   using H = Hist<kPacked>;
   constexpr int kHStride = H::kStride;
@@ -272,8 +289,11 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
 
   if (tid < 16) {
     const int row = r0 + tid;
-    st_mode[tid] = row >= p.T ? kNone : (row + 1 > k_eff ? kActive : kTrivial);
-    st_need[tid] = k_eff;
+    int k = sa.k_eff;
+    if constexpr (kPhase == 2) k = row < p.T ? sa.k_rows[(int64_t)b * p.T + row] : 1;
+    // phase 1 scores every row (each row's variance enters the global mean)
+    st_mode[tid] = row >= p.T ? kNone : ((kPhase == 1 || row + 1 > k) ? kActive : kTrivial);
+    st_need[tid] = k;
   }
   if (tid < 2) st_any[tid] = 0;
   __syncthreads();
@@ -281,16 +301,17 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
 
   // Every chunk after the diagonal tile is zero; trivial rows get their
   // causal prefix now.  (The zeroing is largest for the lightest groups.)
+  // Phase 1 writes no mask.
   const int ntl = rg_idx + 1;                  // causal 16-key tiles 0 .. rg_idx
   const int zend = (rg_idx | 3) + 1;           // chunks up to the end of the 64-key tile
-  for (int i = tid; i < 16 * zend; i += 256) {
-    const int rl = i / zend, tile = i % zend;
-    const int row = r0 + rl;
-    if (row >= p.T) continue;
-    if (tile >= ntl) b16[row * row16 + tile] = 0;
-    else if (st_mode[rl] == kTrivial) b16[row * row16 + tile] = prefix_chunk(row, tile);
-  }
-  {
+  if (kPhase != 1) {
+    for (int i = tid; i < 16 * zend; i += 256) {
+      const int rl = i / zend, tile = i % zend;
+      const int row = r0 + rl;
+      if (row >= p.T) continue;
+      if (tile >= ntl) b16[row * row16 + tile] = 0;
+      else if (st_mode[rl] == kTrivial) b16[row * row16 + tile] = prefix_chunk(row, tile);
+    }
     const int W = 2 * ((p.T + 63) >> 6);
     const int d0 = zend >> 2;                    // first 8-byte pair of words past the 64-key tile
     const int npair = (W >> 1) - d0;
@@ -342,31 +363,37 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
     __syncthreads();
   };
 
-  zero_hist();
-  {
-    typename Mfma<T>::Op kb[Mfma<T>::kSteps], kn[Mfma<T>::kSteps];
-    int t = wave;
-    if (t < ntl) rgp.load_keys(t * 16, p.T, lane, kn);
-    for (; t < ntl; t += kGroupWaves) {
+  if constexpr (kPhase == 2) {
+    // histograms of phase 1 (same grid, so the same block index)
+    const uint32_t* hsrc = sa.hist + (int64_t)blockIdx.x * (16 * kHStride);
+    for (int i = tid; i < 16 * kHStride; i += 256) sh[i] = hsrc[i];
+  } else {
+    zero_hist();
+    {
+      typename Mfma<T>::Op kb[Mfma<T>::kSteps], kn[Mfma<T>::kSteps];
+      int t = wave;
+      if (t < ntl) rgp.load_keys(t * 16, p.T, lane, kn);
+      for (; t < ntl; t += kGroupWaves) {
 #pragma unroll
-      for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = kn[s];
-      if (t + kGroupWaves < ntl) rgp.load_keys((t + kGroupWaves) * 16, p.T, lane, kn);
-      floatx4 acc[kHi];
-      rgp.mma(kb, acc);
-      bool valid[4];
-      slot_valid(t * 16 + lr, valid);
-      floatx4 sc;
+        for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = kn[s];
+        if (t + kGroupWaves < ntl) rgp.load_keys((t + kGroupWaves) * 16, p.T, lane, kn);
+        floatx4 acc[kHi];
+        rgp.mma(kb, acc);
+        bool valid[4];
+        slot_valid(t * 16 + lr, valid);
+        floatx4 sc;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sc[e] = rgp.score(acc, e);
-        const int bn = valid[e] ? bin_of(sc[e], inv_w[e]) : kNB;
-        H::add(&sh[(4 * g + e) * kHStride], bn);
+        for (int e = 0; e < 4; ++e) {
+          sc[e] = rgp.score(acc, e);
+          const int bn = valid[e] ? bin_of(sc[e], inv_w[e]) : kNB;
+          H::add(&sh[(4 * g + e) * kHStride], bn);
+        }
+        *reinterpret_cast<floatx4*>(wsg + t * kTile + lane * 4) = sc;
       }
-      *reinterpret_cast<floatx4*>(wsg + t * kTile + lane * 4) = sc;
     }
   }
   __syncthreads();
-  if (tid < 16 && st_mode[tid] == kActive) {
+  if (kPhase != 1 && tid < 16 && st_mode[tid] == kActive) {
     int nd = st_need[tid];
     st_b1[tid] = scan_row(tid, nd);
     st_need[tid] = nd;
@@ -415,6 +442,77 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, int k_eff,
       }
     }
   };
+
+  if constexpr (kPhase == 1) {
+    // ---- row variance (population, over the row's causal scores) --------------
+    // Sums of d = s - c and d^2 with c = the row's mean estimated from its
+    // histogram (bin centres; |mean - c| <= half a bin), so that the
+    // difference S2/n - (S1/n)^2 keeps its precision.  Then the histograms
+    // are saved for phase 2.
+    __shared__ float st_shift[16];
+    __shared__ float2 st_part[16 * kGroupWaves];
+    if (wave == 0 && lr == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st_shift[4 * g + e] = inv_w[e];   // 1 / bin width
+    }
+    __syncthreads();
+    {
+      const int rl = tid >> 4, part = tid & 15;   // 16 threads per row, 32 bins each
+      float m = 0.f;
+      for (int bin = part * (kNB / 16); bin < (part + 1) * (kNB / 16); ++bin)
+        m = __builtin_fmaf((float)H::count(&sh[rl * kHStride], bin), (float)bin + 0.5f, m);
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) m += __shfl_xor(m, o, 64);
+      const int row = r0 + rl;
+      const float iw = st_shift[rl];
+      __syncthreads();
+      if (part == 0) st_shift[rl] = row < p.T ? m / ((float)(row + 1) * iw) : 0.f;
+    }
+    __syncthreads();
+    float c[4], s1[4], s2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      c[e] = st_shift[4 * g + e];
+      s1[e] = 0.f;
+      s2[e] = 0.f;
+    }
+    replay(
+        [&](int, int, int, const bool (&valid)[4], const float (&sc)[4]) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float d = valid[e] ? sc[e] - c[e] : 0.f;
+            s1[e] += d;
+            s2[e] = __builtin_fmaf(d, d, s2[e]);
+          }
+        },
+        [](int) {});
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        s1[e] += __shfl_xor(s1[e], o, 64);
+        s2[e] += __shfl_xor(s2[e], o, 64);
+      }
+    if (lr == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st_part[(4 * g + e) * kGroupWaves + wave] = make_float2(s1[e], s2[e]);
+    }
+    __syncthreads();
+    if (tid < 16 && r0 + tid < p.T) {
+      float S1 = 0.f, S2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < kGroupWaves; ++w) {
+        S1 += st_part[tid * kGroupWaves + w].x;
+        S2 += st_part[tid * kGroupWaves + w].y;
+      }
+      const float n = (float)(r0 + tid + 1);
+      const float m1 = S1 / n;
+      sa.row_var[(int64_t)b * p.T + r0 + tid] = fmaxf(S2 / n - m1 * m1, 0.f);
+    }
+    uint32_t* hdst = sa.hist + (int64_t)blockIdx.x * (16 * kHStride);
+    for (int i = tid; i < 16 * kHStride; i += 256) hdst[i] = sh[i];
+    return;
+  }
 
   // ---- pass 2: bins above b1 -> mask words; bin b1 -> candidates -------------
   // Candidates of row 4g+e found by this wave go to its own region of the
@@ -657,6 +755,37 @@ __global__ __launch_bounds__(256) void bits_to_indices_kernel(const uint32_t* __
   if (tid == 0) count_out[row] = n;
 }
 
+// ---------------------------------------------------------------------------
+// Variance-based adaptive k (gsa_explained.ipynb:577-592): with avg = the mean
+// of every row's variance over all B*T rows (clamped to >= 1e-6),
+//   k_t = clamp(floor(k_base * avg / max(var_t, 1e-6)), k_min, k_max),
+// then capped at k_cap = min(k_max, T).  One block; the sum runs in double in
+// a fixed order (deterministic), the per-row rule in fp32 in the formula's
+// order (k_base * avg, then the correctly rounded division).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void adaptive_k_kernel(const float* __restrict__ var, int n, int k_base,
+                                                          int k_min, int k_max, int k_cap,
+                                                          int* __restrict__ k_rows) {
+  __shared__ double part[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  double sum = 0.0;
+  for (int i = tid; i < n; i += 1024) sum += (double)var[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  if (lane == 0) part[wave] = sum;
+  __syncthreads();
+  double tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) tot += part[w];
+  const float avg = fmaxf((float)(tot / (double)n), 1e-6f);
+  const float num = (float)k_base * avg;
+  for (int i = tid; i < n; i += 1024) {
+    const float r = floorf(num / fmaxf(var[i], 1e-6f));
+    const float c = fminf(fmaxf(r, (float)k_min), (float)k_max);
+    k_rows[i] = min((int)c, k_cap);
+  }
+}
+
 }  // namespace gsa
 
 // ---------------------------------------------------------------------------
@@ -711,6 +840,26 @@ extern "C" int gsa_indexer_scores(const void* q_idx, int64_t q_sb, int64_t q_st,
   return launch_status();
 }
 
+// One launch of the fused selector in phase kPhase; the 16-bit histogram
+// counts are exact while a row has at most 65535 keys.
+template <int kPhase>
+static void launch_bits(const gsa::IdxArgs& a, const gsa::SelArgs& sa, int dtype, uint32_t* bits,
+                        int64_t b_sb, int64_t b_st, float* wsf, uint2* wsc, hipStream_t s) {
+  const bool packed = a.T <= 65535;
+  const dim3 grid(a.B * ((a.T + 15) / 16)), block(256);
+  if (dtype == GSA_DTYPE_BF16) {
+    if (packed)
+      hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, true, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);
+    else
+      hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, false, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);
+  } else {
+    if (packed)
+      hipLaunchKernelGGL((gsa::indexer_bits_kernel<float, true, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);
+    else
+      hipLaunchKernelGGL((gsa::indexer_bits_kernel<float, false, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);
+  }
+}
+
 // Score tiles (1 KiB per causal 16x16 tile), then the candidate lists
 // (16 rows x kCap (key, index) pairs per 16-row group).
 static size_t score_ws_bytes(int B, int T) {
@@ -724,6 +873,31 @@ extern "C" size_t gsa_indexer_select_workspace_bytes(int B, int T) {
   return score_ws_bytes(B, T) + (size_t)B * g * 16 * gsa::kCap * sizeof(uint2);
 }
 
+int gsa_host::launch_adaptive_k(const float* var, int n, int k_base, int k_min, int k_max, int k_cap,
+                                int32_t* k_rows, hipStream_t stream) {
+  hipLaunchKernelGGL(gsa::adaptive_k_kernel, dim3(1), dim3(1024), 0, stream, var, n, k_base, k_min, k_max, k_cap,
+                     k_rows);
+  return launch_status();
+}
+
+// Argument checks shared by the fixed and the adaptive selector.
+static int check_select_args(const void* q_idx, int64_t q_sb, int64_t q_st, const void* k_idx, int64_t k_sb,
+                             int64_t k_st, const void* w, const float* bias, int B, int T, int Hi, int di,
+                             int dtype, const uint32_t* bits, int64_t b_sb, int64_t b_st,
+                             const int32_t* idx_out, const int32_t* count_out, const void* ws) {
+  int st = check_indexer_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype);
+  if (st) return st;
+  if (!bits || !ws) return GSA_ERR_NULL;
+  if ((idx_out == nullptr) != (count_out == nullptr)) return GSA_ERR_NULL;
+  const int W = 2 * ((T + 63) / 64);
+  if (b_st < W || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
+  if (!aligned(bits, 8) || (b_st % 2) || (b_sb % 2)) return GSA_ERR_ALIGN;
+  if (idx_out && (!aligned(idx_out, 4) || !aligned(count_out, 4))) return GSA_ERR_ALIGN;
+  if ((int64_t)B * T > 0x7fffffffLL) return GSA_ERR_SHAPE;
+  if (!aligned(ws, 16)) return GSA_ERR_ALIGN;
+  return GSA_OK;
+}
+
 extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                                   const void* k_idx, int64_t k_sb, int64_t k_st,
                                   const void* w, int64_t w_sb, int64_t w_st,
@@ -732,39 +906,79 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                                   uint32_t* bits, int64_t b_sb, int64_t b_st,
                                   int32_t* idx_out, int32_t* count_out,
                                   void* ws, size_t ws_bytes, void* stream) {
-  int st = check_indexer_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype);
+  int st = check_select_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype, bits, b_sb,
+                             b_st, idx_out, count_out, ws);
   if (st) return st;
-  if (!bits || !ws) return GSA_ERR_NULL;
-  if ((idx_out == nullptr) != (count_out == nullptr)) return GSA_ERR_NULL;
   if (k_eff < 1 || k_eff > T) return GSA_ERR_K;
-  const int W = 2 * ((T + 63) / 64);
-  if (b_st < W || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
-  if (!aligned(bits, 8) || (b_st % 2) || (b_sb % 2)) return GSA_ERR_ALIGN;
-  if (idx_out && (!aligned(idx_out, 4) || !aligned(count_out, 4))) return GSA_ERR_ALIGN;
-  if ((int64_t)B * T > 0x7fffffffLL) return GSA_ERR_SHAPE;
   if (ws_bytes < gsa_indexer_select_workspace_bytes(B, T)) return GSA_ERR_SHAPE;
-  if (!aligned(ws, 16)) return GSA_ERR_ALIGN;
   gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
-  const int ngroups = (T + 15) / 16;
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* wsf = static_cast<float*>(ws);
   uint2* wsc = reinterpret_cast<uint2*>(static_cast<char*>(ws) + score_ws_bytes(B, T));
-  const bool packed = T <= 65535;   // 16-bit histogram counts are exact
-  const dim3 grid(B * ngroups), block(256);
-  if (dtype == GSA_DTYPE_BF16) {
-    if (packed)
-      hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, true>), grid, block, 0, s, a, k_eff, bits, b_sb, b_st, wsf, wsc);
-    else
-      hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, false>), grid, block, 0, s, a, k_eff, bits, b_sb, b_st, wsf, wsc);
-  } else {
-    if (packed)
-      hipLaunchKernelGGL((gsa::indexer_bits_kernel<float, true>), grid, block, 0, s, a, k_eff, bits, b_sb, b_st, wsf, wsc);
-    else
-      hipLaunchKernelGGL((gsa::indexer_bits_kernel<float, false>), grid, block, 0, s, a, k_eff, bits, b_sb, b_st, wsf, wsc);
-  }
+  gsa::SelArgs sa{k_eff, nullptr, nullptr, nullptr};
+  launch_bits<0>(a, sa, dtype, bits, b_sb, b_st, wsf, wsc, s);
   st = launch_status();
   if (st || !idx_out) return st;
+  const int W = 2 * ((T + 63) / 64);
   hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_eff,
+                     idx_out, count_out);
+  return launch_status();
+}
+
+// Adaptive workspace: the fixed selector's, then the phase-1 histograms (16
+// rows x Hist::kStride words per 16-row group), then the per-row variances
+// and k values ([B*T] each, used when the caller does not take them).
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+static size_t hist_ws_bytes(int B, int T) {
+  const size_t g = (size_t)((T + 15) / 16);
+  const size_t stride = T <= 65535 ? gsa::Hist<true>::kStride : gsa::Hist<false>::kStride;
+  return (size_t)B * g * 16 * stride * sizeof(uint32_t);
+}
+
+extern "C" size_t gsa_indexer_select_adaptive_workspace_bytes(int B, int T) {
+  if (B < 1 || T < 1) return 0;
+  return align256(gsa_indexer_select_workspace_bytes(B, T)) + align256(hist_ws_bytes(B, T)) +
+         2 * align256((size_t)B * T * sizeof(float));
+}
+
+extern "C" int gsa_indexer_select_adaptive(const void* q_idx, int64_t q_sb, int64_t q_st,
+                                           const void* k_idx, int64_t k_sb, int64_t k_st,
+                                           const void* w, int64_t w_sb, int64_t w_st,
+                                           const float* bias, float scale,
+                                           int B, int T, int Hi, int di,
+                                           int k_base, int k_min, int k_max, int dtype,
+                                           uint32_t* bits, int64_t b_sb, int64_t b_st,
+                                           int32_t* idx_out, int32_t* count_out,
+                                           int32_t* k_out, float* var_out,
+                                           void* ws, size_t ws_bytes, void* stream) {
+  int st = check_select_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype, bits, b_sb,
+                             b_st, idx_out, count_out, ws);
+  if (st) return st;
+  if (k_base < 1 || k_min < 1 || k_max < k_min) return GSA_ERR_K;
+  if ((k_out && !aligned(k_out, 4)) || (var_out && !aligned(var_out, 4))) return GSA_ERR_ALIGN;
+  if (ws_bytes < gsa_indexer_select_adaptive_workspace_bytes(B, T)) return GSA_ERR_SHAPE;
+  const int k_cap = k_max < T ? k_max : T;
+  gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(ws);
+  float* wsf = reinterpret_cast<float*>(base);
+  uint2* wsc = reinterpret_cast<uint2*>(base + score_ws_bytes(B, T));
+  size_t off = align256(gsa_indexer_select_workspace_bytes(B, T));
+  uint32_t* hist = reinterpret_cast<uint32_t*>(base + off);
+  off += align256(hist_ws_bytes(B, T));
+  float* var = var_out ? var_out : reinterpret_cast<float*>(base + off);
+  off += align256((size_t)B * T * sizeof(float));
+  int32_t* krow = k_out ? k_out : reinterpret_cast<int32_t*>(base + off);
+
+  launch_bits<1>(a, gsa::SelArgs{0, nullptr, var, hist}, dtype, bits, b_sb, b_st, wsf, wsc, s);
+  if ((st = launch_status())) return st;
+  if ((st = launch_adaptive_k(var, B * T, k_base, k_min, k_max, k_cap, krow, s))) return st;
+  launch_bits<2>(a, gsa::SelArgs{0, krow, nullptr, hist}, dtype, bits, b_sb, b_st, wsf, wsc, s);
+  st = launch_status();
+  if (st || !idx_out) return st;
+  const int W = 2 * ((T + 63) / 64);
+  hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_cap,
                      idx_out, count_out);
   return launch_status();
 }

@@ -46,8 +46,12 @@ __device__ __forceinline__ void block_rank2(SelShared& sm, bool p0, bool p1, int
   __syncthreads();   // wave_cnt is reused by the next chunk
 }
 
+// Output rows are `width` entries wide.  Row r selects k = width entries, or
+// k = min(k_rows[r], width) when k_rows is given; entries k .. width-1 of a
+// row are then index 0 with mask 0.
 __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
-    const float* __restrict__ S, int64_t s_sb, int64_t s_st, int T, int Tkv, int k, int order,
+    const float* __restrict__ S, int64_t s_sb, int64_t s_st, int T, int Tkv, int width,
+    const int32_t* __restrict__ k_rows, int order,
     int32_t* __restrict__ idx_out, int32_t* __restrict__ count_out, uint8_t* __restrict__ mask_out) {
   __shared__ SelShared sm;
   extern __shared__ uint64_t sort_buf[];   // GSA_ORDER_SCORE_DESC only
@@ -56,6 +60,7 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
   const int b = row / T, t = row % T;
   const float* srow = S + b * s_sb + (int64_t)t * s_st;
   const int tid = threadIdx.x;
+  const int k = k_rows ? min(k_rows[row], width) : width;
 
   // ---- radix select: 4 passes of 8 bits, MSB first ----
   if (tid == 0) { sm.prefix = 0u; sm.need = k; }
@@ -84,7 +89,11 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
   const uint32_t theta = sm.prefix;
   const int tie_need = sm.need;
 
-  const int64_t obase = (int64_t)row * k;
+  const int64_t obase = (int64_t)row * width;
+  for (int i = k + tid; i < width; i += kSelThreads) {
+    idx_out[obase + i] = 0;
+    if (mask_out) mask_out[obase + i] = 0;
+  }
   if (order == GSA_ORDER_INDEX_ASC) {
     // Sweep 1 writes valid selected entries, sweep 2 the invalid ones after them.
     int n_valid = 0;
@@ -171,6 +180,48 @@ __global__ __launch_bounds__(kSelThreads) void topk_select_kernel(
   }
 }
 
+// Population variance of each row's finite (not -inf) scores, two passes
+// (mean, then squared deviations) as the variance rule states it
+// (gsa_explained.ipynb:577-592); a row without finite scores gets 0.
+__global__ __launch_bounds__(256) void row_var_kernel(const float* __restrict__ S, int64_t s_sb, int64_t s_st,
+                                                      int T, int Tkv, float* __restrict__ var) {
+  __shared__ float part[4];
+  __shared__ int cpart[4];
+  const int row = blockIdx.x;
+  const int b = row / T, t = row % T;
+  const float* srow = S + b * s_sb + (int64_t)t * s_st;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float sum = 0.f;
+  int cnt = 0;
+  for (int j = tid; j < Tkv; j += 256) {
+    const float v = srow[j];
+    if (v != -__builtin_inff()) { sum += v; ++cnt; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    sum += __shfl_xor(sum, o, 64);
+    cnt += __shfl_xor(cnt, o, 64);
+  }
+  if (lane == 0) { part[wave] = sum; cpart[wave] = cnt; }
+  __syncthreads();
+  const float n = (float)max(1, cpart[0] + cpart[1] + cpart[2] + cpart[3]);
+  const float mean = (((part[0] + part[1]) + part[2]) + part[3]) / n;
+  __syncthreads();
+  float sq = 0.f;
+  for (int j = tid; j < Tkv; j += 256) {
+    const float v = srow[j];
+    if (v != -__builtin_inff()) {
+      const float d = v - mean;
+      sq = __builtin_fmaf(d, d, sq);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+  if (lane == 0) part[wave] = sq;
+  __syncthreads();
+  if (tid == 0) var[row] = (((part[0] + part[1]) + part[2]) + part[3]) / n;
+}
+
 }  // namespace gsa
 
 using namespace gsa_host;
@@ -195,6 +246,36 @@ extern "C" int gsa_topk_select(const float* scores, int64_t s_sb, int64_t s_st,
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(gsa::topk_select_kernel, dim3(B * T), dim3(gsa::kSelThreads), dyn, s, scores, s_sb,
-                     s_st, T, Tkv, k_eff, order, idx_out, count_out, mask_out);
+                     s_st, T, Tkv, k_eff, nullptr, order, idx_out, count_out, mask_out);
+  return launch_status();
+}
+
+extern "C" int gsa_topk_select_adaptive(const float* scores, int64_t s_sb, int64_t s_st,
+                                        int B, int T, int Tkv, int k_base, int k_min, int k_max, int order,
+                                        int32_t* idx_out, int32_t* count_out, uint8_t* mask_out,
+                                        int32_t* k_out, float* var_out, void* stream) {
+  if (!scores || !idx_out || !k_out || !var_out) return GSA_ERR_NULL;
+  if (B < 1 || T < 1 || Tkv < 1) return GSA_ERR_SHAPE;
+  if (order != GSA_ORDER_INDEX_ASC && order != GSA_ORDER_SCORE_DESC) return GSA_ERR_FLAGS;
+  if (k_base < 1 || k_min < 1 || k_max < k_min) return GSA_ERR_K;
+  const int width = k_max < Tkv ? k_max : Tkv;
+  if (order == GSA_ORDER_SCORE_DESC && width > GSA_TOPK_DESC_MAX_K) return GSA_ERR_K;
+  if (!aligned(scores, 4) || !aligned(idx_out, 4) || (count_out && !aligned(count_out, 4)) ||
+      !aligned(k_out, 4) || !aligned(var_out, 4))
+    return GSA_ERR_ALIGN;
+  if ((int64_t)B * T > 0x7fffffffLL) return GSA_ERR_SHAPE;
+  size_t dyn = 0;
+  if (order == GSA_ORDER_SCORE_DESC) {
+    int kp = 1;
+    while (kp < width) kp <<= 1;
+    dyn = (size_t)kp * sizeof(uint64_t);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(gsa::row_var_kernel, dim3(B * T), dim3(256), 0, s, scores, s_sb, s_st, T, Tkv, var_out);
+  int st = launch_status();
+  if (st) return st;
+  if ((st = launch_adaptive_k(var_out, B * T, k_base, k_min, k_max, width, k_out, s))) return st;
+  hipLaunchKernelGGL(gsa::topk_select_kernel, dim3(B * T), dim3(gsa::kSelThreads), dyn, s, scores, s_sb,
+                     s_st, T, Tkv, width, k_out, order, idx_out, count_out, mask_out);
   return launch_status();
 }

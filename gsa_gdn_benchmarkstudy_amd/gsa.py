@@ -25,16 +25,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _abi
-
-try:  # roctx ranges on ROCm builds of torch; no-ops elsewhere
-    from torch.cuda import nvtx as _nvtx
-    _range_push, _range_pop = _nvtx.range_push, _nvtx.range_pop
-except Exception:  # pragma: no cover
-    def _range_push(msg: str):
-        pass
-
-    def _range_pop():
-        pass
+from .roctx import range_pop as _range_pop, range_push as _range_push
 
 
 # Width of the fused projection output is padded to a multiple of this many
@@ -175,17 +166,47 @@ class GatedLightningIndexer(nn.Module):
 
 
 class AdaptiveTopKSelector(nn.Module):
-    """Fixed k_eff = min(k_base, k_max, T_kv); k_min is kept but unused, as in
-    the reference (gsa_opt.py:466-483)."""
+    """Per-row top-k selector (gsa_opt.py:466-483).
+
+    ``mode = "fixed"`` (default, the reference's behaviour): every row takes
+    k_eff = min(k_base, k_max, T_kv); k_min is kept but unused.
+
+    ``mode = "variance"``: the variance-based rule of gsa_explained.ipynb:577-592.
+    Row t takes k_t = min(clamp(floor(k_base * avg / var_t), k_min, k_max), T_kv),
+    var_t the population variance of its finite scores and avg the mean of var_t
+    over all rows of the batch (both clamped to >= 1e-6).  Outputs are then
+    min(k_max, T_kv) wide, entries past k_t masked out; ``last_k`` holds the
+    per-row k of the latest call (int32 [B,T], on the device).
+    """
+
+    MODES = ("fixed", "variance")
 
     def __init__(self, k_base: int = 2048, k_min: int = 256, k_max: int = 4096):
         super().__init__()
         self.k_base = k_base
         self.k_min = k_min
         self.k_max = k_max
+        self.mode = "fixed"
+        self.last_k: Optional[torch.Tensor] = None
+
+    def adaptive(self) -> bool:
+        if self.mode not in self.MODES:
+            raise ValueError(f"selector mode {self.mode!r}: expected one of {self.MODES}")
+        return self.mode == "variance"
 
     def k_effective(self, t_kv: int) -> int:
+        """Output width: k_eff (fixed mode) or min(k_max, T_kv) (variance mode)."""
+        if self.adaptive():
+            return min(self.k_max, t_kv)
         return min(self.k_base, self.k_max, t_kv)
+
+    def _select(self, s: torch.Tensor, k_eff: int, order: int, want_mask: bool = True):
+        if self.adaptive():
+            idx, cnt, mask, k_rows, _ = _abi.topk_select_adaptive(s, self.k_base, self.k_min, self.k_max,
+                                                                  order, want_mask=want_mask)
+            self.last_k = k_rows
+            return idx, cnt, mask
+        return _abi.topk_select(s, k_eff, order, want_mask=want_mask)
 
     def forward(self, scores: torch.Tensor):
         """(indices int64 [B,T,k] by (score desc, index asc), mask bool, k_eff)."""
@@ -196,10 +217,10 @@ class AdaptiveTopKSelector(nn.Module):
         _range_push("gsa_hip/topk_select")
         try:
             if k_eff <= _abi.TOPK_DESC_MAX_K:
-                idx, _, mask = _abi.topk_select(s, k_eff, _abi.ORDER_SCORE_DESC, want_mask=True)
+                idx, _, mask = self._select(s, k_eff, _abi.ORDER_SCORE_DESC)
                 return idx.long(), mask.bool(), k_eff
             # larger k: exact selection in index order, then a stable device sort by score
-            idx, _, mask = _abi.topk_select(s, k_eff, _abi.ORDER_INDEX_ASC, want_mask=True)
+            idx, _, mask = self._select(s, k_eff, _abi.ORDER_INDEX_ASC)
             idx = idx.long()
             vals = torch.gather(s, -1, idx).masked_fill(~mask.bool(), -1e9)
             order = torch.sort(vals, dim=-1, descending=True, stable=True).indices
@@ -211,7 +232,7 @@ class AdaptiveTopKSelector(nn.Module):
     def select_ascending(self, scores: torch.Tensor):
         """(idx int32 [B,T,k] valid-ascending, count int32 [B,T], k_eff)."""
         k_eff = self.k_effective(scores.shape[-1])
-        idx, cnt, _ = _abi.topk_select(scores, k_eff, _abi.ORDER_INDEX_ASC)
+        idx, cnt, _ = self._select(scores, k_eff, _abi.ORDER_INDEX_ASC, want_mask=False)
         return idx, cnt, k_eff
 
 
@@ -390,12 +411,18 @@ class GatedSparseAttention(nn.Module):
         bits: the selection bitmask int32 [B,T,2*ceil(T/64)]; idx/count
         (ascending int32, per-row count) only when ``indices``.
         """
-        k_eff = self.topk_selector.k_effective(T)
+        sel = self.topk_selector
         bias = self._idx_bias32
         if bias is None or bias.device != views["iq"].device:
             bias = self._idx_bias32 = self.indexer.idx_bias.detach().float().contiguous()
-        return _abi.indexer_select(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale, k_eff,
-                                   indices=indices)
+        if sel.adaptive():
+            bits, idx, cnt, k_rows, _ = _abi.indexer_select_adaptive(
+                views["iq"], views["ik"], views["iw"], bias, self.indexer.scale, sel.k_base, sel.k_min,
+                sel.k_max, indices=indices)
+            sel.last_k = k_rows
+            return bits, idx, cnt
+        return _abi.indexer_select(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale,
+                                   sel.k_effective(T), indices=indices)
 
     def uses_dense(self, dtype: torch.dtype) -> bool:
         if self.attn_impl not in ("auto", "dense", "gather"):

@@ -99,6 +99,25 @@ int gsa_topk_select(const float* scores, int64_t s_sb, int64_t s_st,
                     void* stream);
 
 /*
+ * gsa_topk_select with the variance-based per-row k of gsa_explained.ipynb:
+ * 577-592 (the rule AdaptiveTopKSelector, gsa_triton/gsa_opt.py:466-483,
+ * keeps k_min for but does not apply).  var_out[r] = population variance of
+ * row r's finite scores (two passes: mean, then squared deviations); with avg
+ * their mean over all B*T rows,
+ *   k_out[r] = min(clamp(floor(k_base * max(avg,1e-6) / max(var_out[r],1e-6)), k_min, k_max), Tkv).
+ * Row r then selects k_out[r] entries as gsa_topk_select does; output rows
+ * are W = min(k_max, Tkv) wide and entries k_out[r] .. W-1 are index 0 with
+ * mask 0.  idx_out int32 [B,T,W]; count_out (nullable), k_out int32 [B*T];
+ * var_out float [B*T]; mask_out uint8 [B,T,W] (nullable).  Three launches in
+ * stream order.  GSA_ORDER_SCORE_DESC needs W <= GSA_TOPK_DESC_MAX_K.
+ */
+int gsa_topk_select_adaptive(const float* scores, int64_t s_sb, int64_t s_st,
+                             int B, int T, int Tkv, int k_base, int k_min, int k_max, int order,
+                             int32_t* idx_out, int32_t* count_out, uint8_t* mask_out,
+                             int32_t* k_out, float* var_out,
+                             void* stream);
+
+/*
  * Indexer and selector fused.
  * Replaces the indexer track of the optimized forward (gsa_triton/gsa_opt.py:
  * 663-677: fused_gated_indexer + AdaptiveTopKSelector + ascending sort).
@@ -127,6 +146,39 @@ int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                        int32_t* idx_out, int32_t* count_out,
                        void* ws, size_t ws_bytes,
                        void* stream);
+
+/*
+ * The fused indexer + exact top-k with a per-row k from the score variance:
+ * the variance-based adaptive rule of gsa_explained.ipynb:577-592, which the
+ * reference's AdaptiveTopKSelector (gsa_triton/gsa_opt.py:466-483) stores
+ * k_min for but does not apply.  With var_t the population variance of row
+ * t's causal scores (keys j <= t) and avg the mean of var_t over all B*T rows,
+ *   k_t = min(clamp(floor(k_base * max(avg,1e-6) / max(var_t,1e-6)), k_min, k_max), T)
+ * and row t selects its k_t largest causal scores exactly as gsa_indexer_select
+ * does for a fixed k (ties at the k-th value to the lowest indices).
+ * Outputs: bits as gsa_indexer_select; optionally idx_out int32
+ * [B,T,min(k_max,T)] and count_out int32 [B,T] (count = min(t+1, k_t));
+ * optionally k_out int32 [B*T] (k_t) and var_out float [B*T] (var_t).
+ * Three launches on the stream (scores + variances; the global mean and k_t;
+ * the select), all in stream order.  ws: at least
+ * gsa_indexer_select_adaptive_workspace_bytes(B, T) bytes (16-byte aligned):
+ * gsa_indexer_select's workspace, the per-row histograms kept between the
+ * launches (B * G * 16 KiB for T <= 65535, twice that above), and room for
+ * var and k.  Supported: Hi == 4, di == 64, 1 <= k_min <= k_max, k_base >= 1.
+ */
+size_t gsa_indexer_select_adaptive_workspace_bytes(int B, int T);
+
+int gsa_indexer_select_adaptive(const void* q_idx, int64_t q_sb, int64_t q_st,
+                                const void* k_idx, int64_t k_sb, int64_t k_st,
+                                const void* w, int64_t w_sb, int64_t w_st,
+                                const float* bias, float scale,
+                                int B, int T, int Hi, int di,
+                                int k_base, int k_min, int k_max, int dtype,
+                                uint32_t* bits, int64_t b_sb, int64_t b_st,
+                                int32_t* idx_out, int32_t* count_out,
+                                int32_t* k_out, float* var_out,
+                                void* ws, size_t ws_bytes,
+                                void* stream);
 
 /*
  * Producer pass over the projection output: RoPE on k and the G2 value gate.

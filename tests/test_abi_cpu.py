@@ -111,6 +111,58 @@ def test_indexer_select_validation(lib):
     assert lib.gsa_indexer_select_workspace_bytes(0, 5) == 0
 
 
+def _adaptive(lib, **kw):
+    a = dict(q=P, qsb=0, qst=256, k=P, ksb=0, kst=64, w=P, wsb=0, wst=4, bias=P, scale=0.125,
+             B=1, T=32, Hi=4, di=64, kb=8, kmin=2, kmax=16, dtype=1, bits=P, bsb=0, bst=2, idx=P, cnt=P,
+             kout=P, vout=P, ws=P, nws=NWS_A32)
+    a.update(kw)
+    return lib.gsa_indexer_select_adaptive(
+        a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["w"], a["wsb"], a["wst"], a["bias"],
+        a["scale"], a["B"], a["T"], a["Hi"], a["di"], a["kb"], a["kmin"], a["kmax"], a["dtype"], a["bits"],
+        a["bsb"], a["bst"], a["idx"], a["cnt"], a["kout"], a["vout"], a["ws"], a["nws"], None)
+
+
+# adaptive workspace at B=1, T=32, each part rounded up to 256 bytes: the fixed
+# selector's, the phase-1 histograms (2 groups x 16 rows x 257 packed words),
+# then var and k (128 B each)
+NWS_A32 = NWS_T32 + (2 * 16 * 257 * 4 + 255) // 256 * 256 + 2 * 256
+
+
+def test_indexer_select_adaptive_validation(lib):
+    assert lib.gsa_indexer_select_adaptive_workspace_bytes(1, 32) == NWS_A32
+    hist_unpacked = 4096 * 16 * 513 * 4       # T = 65536: 32-bit counts
+    fixed = lib.gsa_indexer_select_workspace_bytes(1, 65536)
+    assert lib.gsa_indexer_select_adaptive_workspace_bytes(1, 65536) == fixed + hist_unpacked + 2 * 65536 * 4
+    assert lib.gsa_indexer_select_adaptive_workspace_bytes(0, 8) == 0
+    assert _adaptive(lib, bias=None) == 1
+    assert _adaptive(lib, ws=None) == 1
+    assert _adaptive(lib, idx=None) == 1          # count without idx
+    assert _adaptive(lib, kb=0) == 5
+    assert _adaptive(lib, kmin=0) == 5
+    assert _adaptive(lib, kmin=17) == 5           # k_min > k_max
+    assert _adaptive(lib, kout=P + 2) == 4
+    assert _adaptive(lib, nws=NWS_A32 - 1) == 2
+    assert _adaptive(lib, dtype=7) == 3
+
+
+def test_topk_adaptive_validation(lib):
+    f = lib.gsa_topk_select_adaptive
+
+    def call(scores=P, B=1, T=32, Tkv=32, kb=8, kmin=2, kmax=16, order=0, kout=P, vout=P):
+        return f(scores, 0, 32, B, T, Tkv, kb, kmin, kmax, order, P, P, None, kout, vout, None)
+
+    assert call(scores=None) == 1
+    assert call(kout=None) == 1
+    assert call(vout=None) == 1
+    assert call(kmin=0) == 5
+    assert call(kmin=20) == 5
+    assert call(kb=0) == 5
+    assert call(order=3) == 6
+    assert call(T=0) == 2
+    assert call(kout=P + 1) == 4
+    assert call(Tkv=8192, kmax=5000, order=1) == 5   # desc order width cap
+
+
 def test_dense_path_validation(lib):
     f = lib.gsa_selection_mask
     assert f(None, 0, 8, 8, None, None, 1, 4, 4, P, 0, 2, None) == 1

@@ -74,3 +74,15 @@ def test_no_cpu_fallback():
     m = _model()
     with pytest.raises(RuntimeError):
         m(torch.randn(1, 8, CFG.hidden_size))
+
+
+def test_selector_modes():
+    from gsa_gdn_benchmarkstudy_amd import AdaptiveTopKSelector
+
+    s = AdaptiveTopKSelector(k_base=2048, k_min=256, k_max=4096)
+    assert s.mode == "fixed" and s.k_effective(16384) == 2048 and s.k_effective(1000) == 1000
+    s.mode = "variance"          # outputs are min(k_max, T) wide; k_t varies per row
+    assert s.k_effective(16384) == 4096 and s.k_effective(1000) == 1000
+    s.mode = "median"
+    with pytest.raises(ValueError):
+        s.k_effective(10)
