@@ -53,11 +53,13 @@ def synthetic_model(dev, dtype, seed=0):
     return m
 
 
-def attn_bytes(B, T, k_eff, s=2):
+def attn_bytes(B, T, k_eff, s=2, P=None):
     """Algorithmic bytes of one sparse-attention launch: gathered K+V rows of the
     valid selected entries, their int32 indices, the q read and out write, and
-    the output-gate logits."""
-    P = B * sum(min(t + 1, k_eff) for t in range(T))
+    the output-gate logits.  P = number of valid (row, key) pairs, by default
+    B * sum_t min(t+1, k_eff)."""
+    if P is None:
+        P = B * sum(min(t + 1, k_eff) for t in range(T))
     return P * H * DH * 2 * s + 4 * P + 2 * B * T * H * DH * s + B * T * D * s, P
 
 
@@ -138,6 +140,8 @@ def main():
     ap.add_argument("--config", choices=sorted(CONFIGS), default="c3")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--k-mode", choices=["fixed", "variance"], default="fixed",
+                    help="selector: fixed k_eff (the reference) or the variance-based per-row k")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after timing, run one plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -154,6 +158,7 @@ def main():
     B, T = CONFIGS[args.config]
     dtype = torch.bfloat16
     model = synthetic_model(dev, dtype)
+    model.topk_selector.mode = args.k_mode
     g = torch.Generator(device="cpu").manual_seed(1)
     x = torch.randn(B, T, D, generator=g)
     if args.config == "c4":   # per-sequence sigma ~ U(0.5, 2)
@@ -180,6 +185,12 @@ def main():
     ms = total_ms / args.steps
     attn_impl = "dense" if model.uses_dense(dtype) else "gather"
     attn_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    P_sel = k_stats = None
+    if args.k_mode == "variance":
+        kr = model.topk_selector.last_k.cpu().long()
+        P_sel = int(torch.minimum(kr, torch.arange(1, T + 1).view(1, T)).sum())
+        k_stats = {"min": int(kr.min()), "mean": float(kr.float().mean()), "max": int(kr.max()),
+                   "per_batch_mean": [float(v) for v in kr.float().mean(dim=1)]}
 
     # the gather kernel on the same layer and input, timed the same way
     gather_ms = None
@@ -221,7 +232,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    abytes, P = attn_bytes(B, T, k_eff)
+    abytes, P = attn_bytes(B, T, k_eff, P=P_sel)
     gather_gbs = abytes / (gather_ms * 1e-3) / 1e9
     aflops = 4 * P * H * DH                     # useful (selected-pair) QK and PV flops
     fidx = indexer_flops(B, T)
@@ -259,8 +270,10 @@ def main():
         "data": "synthetic: x~N(0,1) (c4: per-sequence sigma~U(0.5,2)), weights~N(0,0.02), gate biases 0.5, "
                 "indexer biases 0, random init",
         "config": {"workload": f"GSA layer forward B={B} T={T} D={D} H={H} d={DH} H_idx={HI} d_idx={DI} "
-                               f"k_eff={k_eff} causal", "name": args.config, "batch": B, "seq_len": T,
-                   "k_eff": k_eff},
+                               + (f"k_eff={k_eff}" if args.k_mode == "fixed" else
+                                  f"variance-adaptive k (k_base={K_BASE}, k_min={K_MIN}, k_max={K_MAX})")
+                               + " causal", "name": args.config, "batch": B, "seq_len": T,
+                   "k_mode": args.k_mode, "k_eff": k_eff if args.k_mode == "fixed" else k_stats},
         "roofline": roofline,
         "gather_attention": gather_roof,
         "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,
