@@ -242,7 +242,7 @@ def main():
                    "traffic": profiled_traffic("gsa_sparse_attn", args.config),
                    "algorithmic_bytes": abytes, "valid_pairs": P, "ms": gather_ms}
     if attn_impl == "dense":
-        qrows = 128                              # query rows per block of gsa_dense_attn
+        qrows = 256                              # query rows per block of gsa_dense_attn
         nqb = (T + qrows - 1) // qrows
         dense_flops = 4 * B * H * DH * qrows * 64 * sum(min(qb * qrows + qrows - 1, T - 1) // 64 + 1
                                                          for qb in range(nqb))

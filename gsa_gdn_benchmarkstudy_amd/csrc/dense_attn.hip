@@ -23,7 +23,8 @@
 
 namespace gsa {
 
-constexpr int kDQ = 128;         // query rows per dense-attention block (32 per wave)
+constexpr int kDW = 8;           // waves per dense-attention block (32 query rows each)
+constexpr int kDQ = 32 * kDW;    // query rows per dense-attention block
 constexpr int kDK = 64;          // keys per tile
 constexpr int kKS = 128 + 8;     // LDS row stride of prologue_vt's staging tile (elements)
 
@@ -188,11 +189,11 @@ constexpr float kLazy = 8.f;           // log2 headroom of the lazy softmax refe
 constexpr int kKRow = 17, kVRow = 9;   // padded row lengths in 16-byte units
 constexpr int kKU = kDK * kKRow;       // 1088 units: K tile
 constexpr int kVU = 128 * kVRow;       // 1152 units: V^T tile
-constexpr int kBufU = kKU + kVU;       // one buffer, 35 KiB
 constexpr int kDmaK = kKU / 64;        // 17 load instructions fill a K tile
 constexpr int kDmaV = kVU / 64;        // 18 fill a V^T tile
-constexpr int kDmaWave = 9;            // per wave and tile: instruction 4n + w, wave 3 repeats the last
-constexpr size_t kDenseLds = 2 * kBufU * 16;
+constexpr int kDmaKW = (kDmaK + kDW - 1) / kDW;   // K instructions per wave (wave w: i = kDW*n + w < 17)
+constexpr int kDmaVW = (kDmaV + kDW - 1) / kDW;   // V^T instructions per wave
+constexpr size_t kDenseLds = (size_t)2 * (kKU + kVU) * 16;   // two K slots, then two V^T slots
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -232,53 +233,27 @@ __device__ __forceinline__ void load_lds16(const void* base, uint32_t voff, uint
 }
 #pragma clang diagnostic pop
 
-// Instruction order of the two pipelined regions of a tile (scheduling
-// hints; data dependences still rule).  S region: 16 K operand reads, the 16
-// MFMAs of S^T(half 0) and S^T(half 1), and the softmax of half 0 between
-// the MFMAs of half 1.  PV region: 8 V^T operand reads and the 8 MFMAs of
-// O^T += V^T P^T(half 0), with the softmax of half 1 between them.  Reads
-// run 4 ahead of the MFMAs that use them.
-__device__ __forceinline__ void sched_s_region() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);      // DS reads
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {                            // S^T(half 0)
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // DS read
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {                            // S^T(half 1) || softmax(half 0)
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);   // VALU
-  }
-}
-__device__ __forceinline__ void sched_pv_region() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {                            // O^T += V^T P^T(half 0) || softmax(half 1)
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
-  }
-}
-__device__ __forceinline__ void sched_mfma_region() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-  }
-}
-
 // s_waitcnt immediate (gfx9 encoding): vmcnt(0), expcnt and lgkmcnt not waited
 constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xf << 8);
 
 __device__ __forceinline__ int swap_bits23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
+template <int N> struct Int { static constexpr int value = N; };
+
+// Pipeline of one block (kDW waves = kDQ query rows of one head), tile t = 64
+// keys.  K tiles and V^T tiles stream through separate pairs of LDS slots
+// (tile t in slot t&1).  Iteration t, after one barrier:
+//   loads  K(t+2) into K slot t&1 (S(t) was computed last iteration) and
+//          V^T(t+1) into V slot (t+1)&1 (PV(t-1) is done);
+//   MFMA   S^T(t+1) from K slot (t+1)&1, interleaved with the softmax of
+//          S(t) (VALU), then O^T += V^T(t) P^T(t) from V slot t&1.
+// So the S product of the next tile overlaps the softmax of this one.  Every
+// load is issued one iteration before the barrier that publishes it; the
+// loop is unrolled by two so that slot offsets are constants.
 // lm is a separate restrict argument: nothing in this kernel writes it, and
 // alias analysis can see that, so its uniform reads stay scalar loads.
-__global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p, const uint64_t* __restrict__ lm) {
-  extern __shared__ __align__(16) u32x4 dsm[];   // two buffers of kBufU units: K tile, then V^T tile
+__global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs p, const uint64_t* __restrict__ lm) {
+  extern __shared__ __align__(16) u32x4 dsm[];   // K slots 0, 1 (kKU units each), then V^T slots 0, 1 (kVU)
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(w);
@@ -294,18 +269,20 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p, const u
 
   const int last_key = (p.flags & kDenseCausal) ? min(p.Tkv - 1, q0 + kDQ - 1) : p.Tkv - 1;
   const int nkt = last_key / kDK + 1;
-  const uint16_t* kbase = p.k + b * p.k_sb + hd * 128;
-  const uint16_t* vtb = p.vt + b * p.vt_sb + hd * p.vt_sh;
+  const char* kbase = reinterpret_cast<const char*>(p.k + b * p.k_sb + hd * 128);
+  const char* vtb = reinterpret_cast<const char*>(p.vt + b * p.vt_sb + hd * p.vt_sh);
+  const int64_t kstep = (int64_t)kDK * p.k_st * 2;             // bytes from one K tile to the next
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(dsm));
 
-  // ---- tile loads: wave w issues instructions i = 4n + w (n < 9) ----------
-  // instruction i < 17 fills K units 64i .. 64i+63 (key u/17, unit u%17),
-  // the others V^T units 64(i-17) .. (row u/9, unit u%9): n < 4 are K loads,
-  // n = 4 is K for wave 0 only, n > 4 are V^T loads (wave 3's last repeats
-  // instruction 34).  doff = this lane's source byte offset from the tile's K
-  // or V^T base (32-bit: the host bounds k_st and ldv); doff_last for the
-  // last tile, whose keys past Tkv-1 re-read key Tkv-1.
-  uint32_t doff[kDmaWave], doff_last[5];
+  // ---- tile loads: wave w issues K instructions i = kDW*n + w < 17 and V^T
+  // instructions i = kDW*n + w < 18.  K instruction i fills K units
+  // 64i .. 64i+63 (key u/17, unit u%17), V^T instruction i units 64i .. (row
+  // u/9, unit u%9).  koff/voff = this lane's source byte offset from the
+  // tile's K or V^T base (32-bit: the host bounds k_st and ldv); koff_last
+  // for the last tile, whose keys past Tkv-1 re-read key Tkv-1.
+  const int nkw = (kDmaK - 1 - wu) / kDW + 1;    // this wave's K instructions (uniform)
+  const int nvw = (kDmaV - 1 - wu) / kDW + 1;    // and V^T instructions
+  uint32_t koff[kDmaKW], koff_last[kDmaKW], voff[kDmaVW];
   {
     const uint32_t kst2 = (uint32_t)p.k_st * 2u, ldv2 = (uint32_t)p.ldv * 2u;
     const int kmax_last = min(kDK - 1, p.Tkv - 1 - (nkt - 1) * kDK);
@@ -313,36 +290,36 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p, const u
       const int u = i * 64 + lane, key = u / kKRow, c = u - key * kKRow;
       return (uint32_t)min(key, kmax) * kst2 + (uint32_t)min(c, 15) * 16u;
     };
-    auto v_off = [&](int iv) {
-      const int u = iv * 64 + lane, d = u / kVRow, c = u - d * kVRow;
-      return (uint32_t)d * ldv2 + (uint32_t)min(c, 7) * 16u;
-    };
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      doff[n] = k_off(4 * n + wu, kDK - 1);
-      doff_last[n] = k_off(4 * n + wu, kmax_last);
+    for (int n = 0; n < kDmaKW; ++n) {
+      const int i = min(kDW * n + wu, kDmaK - 1);
+      koff[n] = k_off(i, kDK - 1);
+      koff_last[n] = k_off(i, kmax_last);
     }
-    doff[4] = wu == 0 ? k_off(16, kDK - 1) : v_off(wu - 1);
-    doff_last[4] = wu == 0 ? k_off(16, kmax_last) : doff[4];
 #pragma unroll
-    for (int n = 5; n < kDmaWave; ++n) doff[n] = v_off(min(4 * n + wu - kDmaK, kDmaV - 1));
+    for (int n = 0; n < kDmaVW; ++n) {
+      const int u = min(kDW * n + wu, kDmaV - 1) * 64 + lane, d = u / kVRow, c = u - d * kVRow;
+      voff[n] = (uint32_t)d * ldv2 + (uint32_t)min(c, 7) * 16u;
+    }
   }
-  auto issue = [&](int kt, int buf) {
-    const int j0 = kt * kDK;
-    const bool last = kt == nkt - 1;
-    const char* kb = reinterpret_cast<const char*>(kbase + (int64_t)j0 * p.k_st);
-    const char* vb = reinterpret_cast<const char*>(vtb + j0);
-    const uint32_t ka = lds0 + (uint32_t)(buf * kBufU * 16);
-    const uint32_t va = ka + kKU * 16;
+  const uint32_t kdst = lds0 + (uint32_t)wu * 1024u;                      // + slot * kKU * 16 + n * kDW KiB
+  const uint32_t vdst = lds0 + (uint32_t)(2 * kKU * 16) + (uint32_t)wu * 1024u;
+  auto issue_k = [&](const char* src, int slot, bool last) {   // one K tile into K slot `slot`
 #pragma unroll
-    for (int n = 0; n < 4; ++n) load_lds16(kb, last ? doff_last[n] : doff[n], ka + (4 * n + wu) * 1024);
-    if (wu == 0) load_lds16(kb, last ? doff_last[4] : doff[4], ka + 16 * 1024);
-    else load_lds16(vb, doff[4], va + (wu - 1) * 1024);
-#pragma unroll
-    for (int n = 5; n < kDmaWave; ++n) load_lds16(vb, doff[n], va + min(4 * n + wu - kDmaK, kDmaV - 1) * 1024);
+    for (int n = 0; n < kDmaKW; ++n)
+      if (n + 1 < kDmaKW || n < nkw)
+        load_lds16(src, last ? koff_last[n] : koff[n], kdst + (uint32_t)(slot * kKU * 16 + n * kDW * 1024));
   };
-  issue(0, 0);
-  if (nkt > 1) issue(1, 1);
+  auto issue_v = [&](const char* src, int slot) {              // one V^T tile into V slot `slot`
+#pragma unroll
+    for (int n = 0; n < kDmaVW; ++n)
+      if (n + 1 < kDmaVW || n < nvw)
+        load_lds16(src, voff[n], vdst + (uint32_t)(slot * kVU * 16 + n * kDW * 1024));
+  };
+  // prologue loads: K(0), K(1), V(0)
+  issue_k(kbase, 0, nkt == 1);
+  if (nkt > 1) issue_k(kbase + kstep, 1, nkt == 2);
+  issue_v(vtb, 0);
 
   // ---- q: B operand of S^T; lane supplies d = 16s + 8h .. +7 of its row ----
   u32x4 qraw[8];
@@ -387,110 +364,121 @@ __global__ __launch_bounds__(256, 2) void dense_attn_kernel(DenseArgs p, const u
     for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
   float m = -__builtin_inff(), l = 0.f;
 
-  // this wave's lane masks: group 4*qb + w (wave index uniform for scalar loads)
-  const uint64_t* lmw = lm + ((int64_t)b * p.G + 4 * qb + wu) * p.NT * 32;
-  // operand read bases (units within a buffer): K row of MFMA row i32, V^T row i32
+  // this wave's lane masks: group kDW*qb + w (wave index uniform for scalar loads)
+  const uint64_t* lmw = lm + ((int64_t)b * p.G + kDW * qb + wu) * p.NT * 32;
+  // operand read offsets (units within a slot): K row of MFMA row i32, V^T row i32
   const int kread = swap_bits23(i32) * kKRow + h;
-  const int vread = kKU + i32 * kVRow + h;
+  const int vread = 2 * kKU + i32 * kVRow + h;
 
-  // The q (and cos/sin) loads have landed.  The wait is the compiler's own
-  // intrinsic, so it knows that none of its loads is still in flight and puts
-  // no vmcnt wait into the loop, where the counter also counts the tile loads
-  // and any such wait would drain them.
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    // this wave's loads of tile kt are done (tile kt+1's may still fly); the
-    // barrier publishes every wave's part
-    if (kt + 1 < nkt) asm volatile("s_waitcnt vmcnt(9)\n\ts_barrier" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    const u32x4* sK = dsm + buf * kBufU + kread;
-    const u32x4* sV = dsm + buf * kBufU + vread;
-    const uint64_t* lmt = lmw + kt * 32;
-
-    auto s_half = [&](int c) {
-      bf16x8 f[8];
+  // S^T of one 32-key half of the tile in K slot ks
+  auto s_half = [&](int ks, int c) {
+    const u32x4* sK = dsm + ks * kKU + kread;
+    bf16x8 f[8];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) f[s] = __builtin_bit_cast(bf16x8, sK[32 * c * kKRow + 2 * s]);
-      floatx16 acc;
+    for (int s = 0; s < 8; ++s) f[s] = __builtin_bit_cast(bf16x8, sK[32 * c * kKRow + 2 * s]);
+    floatx16 acc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[s], qop[s], acc, 0, 0, 0);
-      return acc;
-    };
-    // masked online-softmax step over one half: p = 2^(s*scale*log2e - m)
-    // against a per-row reference m that only moves when the row max exceeds
-    // it by more than kLazy (p <= 2^kLazy; O and l are rescaled rarely; out =
-    // O / l does not depend on m).  Returns P as two B operands of O^T.
-    auto softmax_half = [&](const floatx16& acc, int c, uint32_t (&pk)[2][4], float& alpha) -> bool {
-      float sv[16];
-      float mx = -__builtin_inff();
+    for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[s], qop[s], acc, 0, 0, 0);
+    return acc;
+  };
+  // masked online-softmax step over one half: p = 2^(s*scale*log2e - m)
+  // against a per-row reference m that only moves when the row max exceeds
+  // it by more than kLazy (p <= 2^kLazy; O and l are rescaled rarely; out =
+  // O / l does not depend on m).  Returns P as two B operands of O^T.
+  auto softmax_half = [&](const floatx16& acc, const uint64_t* lmt, int c, uint32_t (&pk)[2][4],
+                          float& alpha) -> bool {
+    float sv[16];
+    float mx = -__builtin_inff();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const bool sel = __builtin_amdgcn_inverse_ballot_w64(lmt[16 * c + r]);
-        sv[r] = sel ? acc[r] : -__builtin_inff();
-        mx = fmaxf(mx, sv[r]);
-      }
-      mx = max_halves(mx) * p.scale_l2;
-      const bool bump = mx > m + kLazy || (m == -__builtin_inff() && mx != -__builtin_inff());
-      const float mref = bump ? mx : m;
-      alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
-      const float msafe = mref == -__builtin_inff() ? 0.f : mref;
-      float lsum = 0.f;
+    for (int r = 0; r < 16; ++r) {
+      const bool sel = __builtin_amdgcn_inverse_ballot_w64(lmt[16 * c + r]);
+      sv[r] = sel ? acc[r] : -__builtin_inff();
+      mx = fmaxf(mx, sv[r]);
+    }
+    mx = max_halves(mx) * p.scale_l2;
+    const bool bump = mx > m + kLazy || (m == -__builtin_inff() && mx != -__builtin_inff());
+    const float mref = bump ? mx : m;
+    alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
+    const float msafe = mref == -__builtin_inff() ? 0.f : mref;
+    float lsum = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], p.scale_l2, -msafe));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r + 1], p.scale_l2, -msafe));
-        pk[r >> 3][(r & 7) >> 1] = cvt_pk_bf16(p0, p1);
-        lsum += p0 + p1;
-      }
-      l = l * alpha + lsum;
-      m = mref;
-      return bump;
-    };
-    auto rescale = [&](float alpha) {
+    for (int r = 0; r < 16; r += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], p.scale_l2, -msafe));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r + 1], p.scale_l2, -msafe));
+      pk[r >> 3][(r & 7) >> 1] = cvt_pk_bf16(p0, p1);
+      lsum += p0 + p1;
+    }
+    l = l * alpha + lsum;
+    m = mref;
+    return bump;
+  };
+  auto rescale = [&](float alpha) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+  };
+  auto pv_half = [&](int vs, int c, const uint32_t (&pk)[2][4]) {
+    const u32x4* sV = dsm + vs * kVU + vread;
+    bf16x8 f[2][4];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
+        f[ks][dt] = __builtin_bit_cast(bf16x8, sV[32 * dt * kVRow + 4 * c + 2 * ks]);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-    };
-    auto pv_half = [&](int c, const uint32_t (&pk)[2][4]) {
-      bf16x8 f[2][4];
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pk[ks][0], pk[ks][1], pk[ks][2], pk[ks][3]});
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-          f[ks][dt] = __builtin_bit_cast(bf16x8, sV[32 * dt * kVRow + 4 * c + 2 * ks]);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pk[ks][0], pk[ks][1], pk[ks][2], pk[ks][3]});
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[ks][dt], pb, o[dt], 0, 0, 0);
-      }
-    };
+      for (int dt = 0; dt < 4; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[ks][dt], pb, o[dt], 0, 0, 0);
+    }
+  };
+
+  // Prologue loads and the q loads have landed.  The wait is the compiler's
+  // own intrinsic, so it knows that none of its loads is still in flight and
+  // puts no vmcnt wait into the loop, where the counter also counts the tile
+  // loads and any such wait would drain them.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  floatx16 sc0 = s_half(0, 0), sc1 = s_half(0, 1);   // S^T of tile 0
+
+  const char* ksrc = kbase + 2 * kstep;              // K tile kt+2
+  const char* vsrc = vtb + kDK * 2;                  // V^T tile kt+1
+  const uint64_t* lmt = lmw;                         // lane masks of tile kt
+  // one iteration; P = kt & 1
+  auto step = [&](int kt, auto par) {
+    constexpr int P = decltype(par)::value;
+    // this wave's loads of K(kt+1) and V^T(kt) (issued last iteration) are
+    // done and its LDS reads have returned; the barrier publishes every
+    // wave's loads and frees K slot P and V slot 1-P
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + 2 < nkt) issue_k(ksrc, P, kt + 3 == nkt);
+    if (kt + 1 < nkt) issue_v(vsrc, 1 - P);
+    ksrc += kstep;
+    vsrc += kDK * 2;
 
     uint32_t pk0[2][4], pk1[2][4];
     float alpha0, alpha1;
-    const floatx16 s0 = s_half(0);
-    const floatx16 s1 = s_half(1);                 // overlaps the softmax of half 0
-    const bool bump0 = softmax_half(s0, 0, pk0, alpha0);
-    sched_s_region();
+    const floatx16 n0 = s_half(1 - P, 0);          // S^T(kt+1) || softmax(kt); stale on the last tile, unused
+    const bool bump0 = softmax_half(sc0, lmt, 0, pk0, alpha0);
+    const floatx16 n1 = s_half(1 - P, 1);
+    const bool bump1 = softmax_half(sc1, lmt, 1, pk1, alpha1);
     if (ballot64(bump0)) rescale(alpha0);
-    pv_half(0, pk0);                               // overlaps the softmax of half 1
-    const bool bump1 = softmax_half(s1, 1, pk1, alpha1);
-    sched_pv_region();
+    pv_half(P, 0, pk0);
     if (ballot64(bump1)) rescale(alpha1);
-    pv_half(1, pk1);
-    sched_mfma_region();
-
-    // every wave is done reading this buffer before it is refilled
-    if (kt + 2 < nkt) {
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      issue(kt + 2, buf);
-    }
+    pv_half(P, 1, pk1);
+    sc0 = n0;
+    sc1 = n1;
+    lmt += 32;
+  };
+  int kt = 0;
+  for (; kt + 1 < nkt; kt += 2) {
+    step(kt, Int<0>{});
+    step(kt + 1, Int<1>{});
   }
+  if (kt < nkt) step(kt, Int<0>{});
 
   // ---- epilogue: normalise, bf16, optional output gate ----
   l = sum_halves(l);
@@ -632,7 +620,7 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
     if (e != hipSuccess) return -static_cast<int>(e);
     g_dense_lds_set[dev] = true;
   }
-  hipLaunchKernelGGL(gsa::dense_attn_kernel, dim3(B * H * nqb), dim3(256), gsa::kDenseLds, s, a,
+  hipLaunchKernelGGL(gsa::dense_attn_kernel, dim3(B * H * nqb), dim3(64 * gsa::kDW), gsa::kDenseLds, s, a,
                      static_cast<const uint64_t*>(lm));
   return launch_status();
 }

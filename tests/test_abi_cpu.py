@@ -171,7 +171,7 @@ def test_dense_path_validation(lib):
     g = lib.gsa_dense_attn
     ok = dict(q=P, qsb=0, qst=2048, k=P, ksb=0, kst=2048, vt=P, vtsb=0, vtsh=8192, ldv=64, bits=P, bsb=0, bst=2,
               og=P, osb=0, ost=2048, cos=P, sin=P, cst=128, out=P, outsb=0, outst=2048,
-              B=1, T=4, Tkv=4, H=16, d=128, scale=0.088, dtype=1, flags=3, causal=1, ws=P, wsb=4 * 256)
+              B=1, T=4, Tkv=4, H=16, d=128, scale=0.088, dtype=1, flags=3, causal=1, ws=P, wsb=8 * 256)
 
     def call(**kw):
         a = dict(ok)
@@ -181,13 +181,13 @@ def test_dense_path_validation(lib):
                  a["out"], a["outsb"], a["outst"], a["B"], a["T"], a["Tkv"], a["H"], a["d"], a["scale"],
                  a["dtype"], a["flags"], a["causal"], a["ws"], a["wsb"], None)
 
-    # 256 B of lane masks per (batch, 32-row group, 64-key tile); groups cover whole 128-row blocks
-    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 4) == 4 * 256
-    assert lib.gsa_dense_attn_workspace_bytes(2, 100, 130) == 2 * 4 * 3 * 256
-    assert lib.gsa_dense_attn_workspace_bytes(1, 129, 64) == 8 * 256
+    # 256 B of lane masks per (batch, 32-row group, 64-key tile); groups cover whole 256-row blocks
+    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 4) == 8 * 256
+    assert lib.gsa_dense_attn_workspace_bytes(2, 100, 130) == 2 * 8 * 3 * 256
+    assert lib.gsa_dense_attn_workspace_bytes(1, 257, 64) == 16 * 256
     assert call(bits=None) == 1
     assert call(ws=None) == 1
-    assert call(wsb=4 * 256 - 1) == 2             # workspace too small
+    assert call(wsb=8 * 256 - 1) == 2             # workspace too small
     assert call(dtype=0) == 3                     # bf16 only
     assert call(ldv=32) == 2                      # rows shorter than ceil(Tkv/64)*64
     assert call(flags=4) == 6
