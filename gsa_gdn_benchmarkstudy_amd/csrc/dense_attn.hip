@@ -123,29 +123,43 @@ __global__ __launch_bounds__(256) void selection_mask_kernel(
 // s = 16c + r (c = 0,1; r = 0..15), lm[b][g][kt][s] bit (32h + i) is the
 // selection bit of row 32g+i and key 64kt + 32c + 16(r/8) + 8h + r%8 -- the
 // key that accumulator r of lane (h, i) holds in the S^T MFMA output of half
-// c (see the key order below).  One wave per (b, g, kt).
+// c (see the key order below).  One wave per (b, g, 4 consecutive tiles):
+// lane (h, i) reads row 32g+i's four 64-bit words, then one ballot per slot
+// transposes them; lanes 0..31 write each tile's 256 contiguous bytes.
 // ---------------------------------------------------------------------------
+constexpr int kLmTiles = 4;
+
 __global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restrict__ bits, int64_t b_sb,
                                                         int64_t b_st, int T, int G, int NT, int nwaves,
                                                         uint64_t* __restrict__ lm) {
   const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (wv >= nwaves) return;
-  const int kt = wv % NT, bg = wv / NT;
+  const int nq = (NT + kLmTiles - 1) / kLmTiles;
+  const int kq = wv % nq, bg = wv / nq;
   const int g = bg % G, b = bg / G;
   const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
   const int row = 32 * g + i;
-  uint64_t word = row < T ? *reinterpret_cast<const uint64_t*>(bits + b * b_sb + (int64_t)row * b_st + 2 * kt) : 0ull;
-  word >>= 8 * h;
-  // lane s collects slot s's mask; lanes 0..31 then write 256 contiguous bytes
-  uint64_t mine = 0ull;
+  const int kt0 = kq * kLmTiles;
+  uint64_t words[kLmTiles];
+  const uint64_t* src = reinterpret_cast<const uint64_t*>(bits + b * b_sb + (int64_t)min(row, T - 1) * b_st) + kt0;
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int u = 0; u < kLmTiles; ++u) words[u] = (row < T && kt0 + u < NT) ? src[u] : 0ull;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint64_t m = ballot64((word >> (32 * c + 16 * (r >> 3) + (r & 7))) & 1ull);
-      mine = lane == 16 * c + r ? m : mine;
-    }
-  if (lane < 32) lm[((int64_t)bg * NT + kt) * 32 + lane] = mine;
+  for (int u = 0; u < kLmTiles; ++u) {
+    if (kt0 + u >= NT) break;
+    const uint64_t word = words[u] >> (8 * h);
+    int lo = 0, hi = 0;                      // slot s's mask lands in lane s
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint64_t m = ballot64((word >> (32 * c + 16 * (r >> 3) + (r & 7))) & 1ull);
+        const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (16 * c + r));   // lane == slot
+        lo = mine ? (int)(uint32_t)m : lo;
+        hi = mine ? (int)(uint32_t)(m >> 32) : hi;
+      }
+    if (lane < 32) lm[((int64_t)bg * NT + kt0 + u) * 32 + lane] = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -602,7 +616,7 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
     return GSA_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint64_t* lm = static_cast<uint64_t*>(ws);
-  const int nwaves = B * G * NT;
+  const int nwaves = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
   hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((nwaves + 3) / 4), dim3(256), 0, s, bits, b_sb, b_st, T, G, NT,
                      nwaves, lm);
   int st = launch_status();
