@@ -33,6 +33,17 @@ from .roctx import range_pop as _range_pop, range_push as _range_push
 FUSED_ALIGN = 64
 
 
+_CU_COUNT = {}
+
+
+def _cu_count(dev: torch.device) -> int:
+    """Compute units of the device (cached)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _CU_COUNT:
+        _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _CU_COUNT[idx]
+
+
 # ---------------------------------------------------------------------------
 # Launchers (gsa_opt.py:143-176, :349-383)
 # ---------------------------------------------------------------------------
@@ -326,6 +337,13 @@ class GatedSparseAttention(nn.Module):
         # with the selection as a bitmask, bf16), "gather" (per-row gather of
         # the selected keys, bf16 and fp32), or "auto" (dense for bf16).
         self.attn_impl = "auto"
+        # Where the fused indexer + top-k runs relative to the main projection
+        # GEMM: "gemm" (on a side stream beside the GEMM), "producer" (after
+        # the GEMM, on a side stream beside the RoPE/gate producer), "serial"
+        # (everything on the current stream) or "auto": "gemm" while the
+        # indexer's grid (one block per 16 query rows) leaves CUs free for the
+        # GEMM -- fewer than 4 blocks per CU -- else "producer".
+        self.indexer_overlap = "auto"
         # Optional per-kernel timing hook: a list to which forward appends
         # (start, end) event pairs around the sparse-attention launch.
         self.attn_events: Optional[list] = None
@@ -447,23 +465,41 @@ class GatedSparseAttention(nn.Module):
 
         dense = self.uses_dense(x.dtype)
 
-        # Track A: indexer projections, then indexer + top-k (+ its bitmask) on
-        # the side stream, concurrent with the main projection GEMM
+        # Track A: the indexer projections, then the fused indexer + top-k
+        # (and its bitmask), on a side stream that starts after the main
+        # projection GEMM ("producer"), right after the small indexer GEMM
+        # ("gemm"), or on the current stream ("serial").  The indexer and the
+        # GEMM both fill the GPU and slow each other down when they share it;
+        # beside the HBM-bound producer the indexer's light tail blocks leave
+        # room for it.
+        mode = self.indexer_overlap
+        if mode == "auto":
+            mode = "gemm" if B * ((T + 15) // 16) < 4 * _cu_count(dev) else "producer"
+        elif mode not in ("producer", "gemm", "serial"):
+            raise ValueError(f"indexer_overlap {mode!r}: expected 'auto', 'producer', 'gemm' or 'serial'")
         _range_push("gsa_hip/indexer_gemm")
         views = self.project_indexer(x)
         _range_pop()
-        if self._indexer_stream is None or self._indexer_stream.device != dev:
-            self._indexer_stream = torch.cuda.Stream(device=dev)
-        side = self._indexer_stream
-        side.wait_stream(cur)
+        if mode == "serial":
+            side = cur
+        else:
+            if self._indexer_stream is None or self._indexer_stream.device != dev:
+                self._indexer_stream = torch.cuda.Stream(device=dev)
+            side = self._indexer_stream
+        if mode == "producer":
+            _range_push("gsa_hip/main_gemm")
+            views.update(self.project_main(x))
+            _range_pop()
+        if side is not cur:
+            side.wait_stream(cur)
         with torch.cuda.stream(side):
             _range_push("gsa_hip/indexer_select")
             bits, idx, cnt = self.select(views, T, indices=not dense)
             _range_pop()
-
-        _range_push("gsa_hip/main_gemm")
-        views.update(self.project_main(x))
-        _range_pop()
+        if mode != "producer":
+            _range_push("gsa_hip/main_gemm")
+            views.update(self.project_main(x))
+            _range_pop()
 
         # Track B: RoPE(k) and the value gate on the current stream
         _range_push("gsa_hip/prologue")
@@ -475,11 +511,12 @@ class GatedSparseAttention(nn.Module):
             k_rope, v_gated = _abi.prologue(k=views["k"], v=views["v"], vg=views["vg"], cos=cos, sin=sin)
         _range_pop()
 
-        cur.wait_stream(side)
-        for t in (idx, cnt, bits):
-            if t is not None:
-                t.record_stream(cur)
-        views["_ibuf"].record_stream(side)
+        if side is not cur:
+            cur.wait_stream(side)
+            for t in (idx, cnt, bits):
+                if t is not None:
+                    t.record_stream(cur)
+            views["_ibuf"].record_stream(side)
 
         _range_push("gsa_hip/sparse_attn")
         ev = None

@@ -209,3 +209,22 @@ def test_layer_repeat_is_deterministic(dev):
         a = m(x)
         b = m(x)
     assert torch.equal(a, b)
+
+
+def test_indexer_overlap_modes_identical(dev):
+    """Every stream arrangement of the indexer (beside the GEMM, beside the
+    producer, serial, auto) computes the same output bit for bit."""
+    cfg = orc.GSAConfig(hidden_size=512, num_heads=4, k_max=96, k_base=64, k_min=16)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=5), torch.bfloat16)
+    x = orc.synthetic_input(2, 300, cfg.hidden_size, seed=6).to(torch.bfloat16).to(dev)
+    m = _model(cfg, sd, dev, torch.bfloat16)
+    outs = []
+    with torch.no_grad():
+        for mode in ("gemm", "producer", "serial", "auto"):
+            m.indexer_overlap = mode
+            outs.append(m(x))
+        m.indexer_overlap = "sideways"
+        with pytest.raises(ValueError):
+            m(x)
+    for y in outs[1:]:
+        assert torch.equal(y, outs[0])
