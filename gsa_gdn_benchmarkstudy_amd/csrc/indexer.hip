@@ -181,9 +181,11 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 //
 // Output: the selection as a bitmask, bits[b][t] bit j set iff key j is one
 // of row t's selected keys (W = 2*ceil(T/64) uint32 words per row; words past
-// row t's causal range are zero).  One 256-thread block per 16-row group,
-// heaviest groups first; its 4 waves take the group's causal 16-key tiles
-// round-robin and share the row state in LDS.  Rows with t+1 <= k select
+// row t's causal range are zero).  One 512-thread block per 16-row group,
+// heaviest groups first; its 8 waves take the group's causal 16-key tiles
+// round-robin and share the row state in LDS (8 rather than 4 waves halve
+// the time of the heaviest groups, which bound the kernel when the whole
+// grid fits the GPU at once).  Rows with t+1 <= k select
 // every causal key.  For the others:
 //   pass 1  MFMA scores -> value-linear histogram, bin = floor(s * NB /
 //           sum_h sigmoid(w_h)), and every score tile is stored to the
@@ -209,9 +211,10 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 // 17 KiB of histograms and can share a CU with a GEMM block).
 // ---------------------------------------------------------------------------
 constexpr int kNB = 512;                 // histogram bins per row
-constexpr int kCap = 512;                // candidates per row
-constexpr int kGroupWaves = 4;
-constexpr int kWCap = kCap / kGroupWaves;  // candidates per row and wave
+constexpr int kGroupWaves = 8;           // waves per 16-row group
+constexpr int kGroupThreads = 64 * kGroupWaves;
+constexpr int kWCap = 128;               // candidates per row and wave
+constexpr int kCap = kWCap * kGroupWaves;  // candidates per row
 
 // Per-row histogram in LDS.  Packed: 512 bins as 16-bit counts, two per
 // word (exact while a row has at most 65535 keys, i.e. T <= 65535), 17 KiB
@@ -264,7 +267,7 @@ struct SelArgs {
 };
 
 template <typename T, bool kPacked, int kPhase>
-__global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, SelArgs sa, uint32_t* bits,
+__global__ __launch_bounds__(kGroupThreads) void indexer_bits_kernel(IdxArgs p, SelArgs sa, uint32_t* bits,
                                                            int64_t b_sb, int64_t b_st, float* ws, uint2* ws_cand) {
   using H = Hist<kPacked>;
   constexpr int kHStride = H::kStride;
@@ -305,7 +308,7 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, SelArgs sa
   const int ntl = rg_idx + 1;                  // causal 16-key tiles 0 .. rg_idx
   const int zend = (rg_idx | 3) + 1;           // chunks up to the end of the 64-key tile
   if (kPhase != 1) {
-    for (int i = tid; i < 16 * zend; i += 256) {
+    for (int i = tid; i < 16 * zend; i += kGroupThreads) {
       const int rl = i / zend, tile = i % zend;
       const int row = r0 + rl;
       if (row >= p.T) continue;
@@ -315,7 +318,7 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, SelArgs sa
     const int W = 2 * ((p.T + 63) >> 6);
     const int d0 = zend >> 2;                    // first 8-byte pair of words past the 64-key tile
     const int npair = (W >> 1) - d0;
-    for (int i = tid; i < 16 * npair; i += 256) {
+    for (int i = tid; i < 16 * npair; i += kGroupThreads) {
       const int rl = i / npair, pr = d0 + i % npair;
       const int row = r0 + rl;
       if (row < p.T) reinterpret_cast<uint2*>(bbase + (int64_t)row * b_st)[pr] = uint2{0u, 0u};
@@ -359,14 +362,14 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, SelArgs sa
     return bsel;
   };
   auto zero_hist = [&]() {
-    for (int i = tid; i < 16 * kHStride; i += 256) sh[i] = 0u;
+    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) sh[i] = 0u;
     __syncthreads();
   };
 
   if constexpr (kPhase == 2) {
     // histograms of phase 1 (same grid, so the same block index)
     const uint32_t* hsrc = sa.hist + (int64_t)blockIdx.x * (16 * kHStride);
-    for (int i = tid; i < 16 * kHStride; i += 256) sh[i] = hsrc[i];
+    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) sh[i] = hsrc[i];
   } else {
     zero_hist();
     {
@@ -457,16 +460,17 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, SelArgs sa
     }
     __syncthreads();
     {
-      const int rl = tid >> 4, part = tid & 15;   // 16 threads per row, 32 bins each
+      const int rl = (tid >> 4) & 15, part = tid & 15;   // threads 0..255: 16 per row, 32 bins each
       float m = 0.f;
-      for (int bin = part * (kNB / 16); bin < (part + 1) * (kNB / 16); ++bin)
-        m = __builtin_fmaf((float)H::count(&sh[rl * kHStride], bin), (float)bin + 0.5f, m);
+      if (tid < 256)
+        for (int bin = part * (kNB / 16); bin < (part + 1) * (kNB / 16); ++bin)
+          m = __builtin_fmaf((float)H::count(&sh[rl * kHStride], bin), (float)bin + 0.5f, m);
 #pragma unroll
       for (int o = 1; o < 16; o <<= 1) m += __shfl_xor(m, o, 64);
       const int row = r0 + rl;
       const float iw = st_shift[rl];
       __syncthreads();
-      if (part == 0) st_shift[rl] = row < p.T ? m / ((float)(row + 1) * iw) : 0.f;
+      if (tid < 256 && part == 0) st_shift[rl] = row < p.T ? m / ((float)(row + 1) * iw) : 0.f;
     }
     __syncthreads();
     float c[4], s1[4], s2[4];
@@ -510,7 +514,7 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, SelArgs sa
       sa.row_var[(int64_t)b * p.T + r0 + tid] = fmaxf(S2 / n - m1 * m1, 0.f);
     }
     uint32_t* hdst = sa.hist + (int64_t)blockIdx.x * (16 * kHStride);
-    for (int i = tid; i < 16 * kHStride; i += 256) hdst[i] = sh[i];
+    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) hdst[i] = sh[i];
     return;
   }
 
@@ -556,10 +560,11 @@ __global__ __launch_bounds__(256) void indexer_bits_kernel(IdxArgs p, SelArgs sa
   // would write back the whole L2.
   __syncthreads();
 
-  // ---- resolve: wave w takes rows 4w .. 4w+3 ----------------------------------
+  // ---- resolve: wave w takes rows kRW*w .. kRW*w + kRW-1 ----------------------
   // Candidate slot i*64 + lane lies in region i/2 at position (i%2)*64 + lane.
-  for (int q = 0; q < 4; ++q) {
-    const int rl = 4 * wave + q;
+  constexpr int kRW = 16 / kGroupWaves;
+  for (int q = 0; q < kRW; ++q) {
+    const int rl = kRW * wave + q;
     if (st_mode[rl] != kActive) continue;
     int nw[kGroupWaves];
     bool ovf = false;
@@ -846,7 +851,7 @@ template <int kPhase>
 static void launch_bits(const gsa::IdxArgs& a, const gsa::SelArgs& sa, int dtype, uint32_t* bits,
                         int64_t b_sb, int64_t b_st, float* wsf, uint2* wsc, hipStream_t s) {
   const bool packed = a.T <= 65535;
-  const dim3 grid(a.B * ((a.T + 15) / 16)), block(256);
+  const dim3 grid(a.B * ((a.T + 15) / 16)), block(gsa::kGroupThreads);
   if (dtype == GSA_DTYPE_BF16) {
     if (packed)
       hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, true, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);

@@ -132,7 +132,7 @@ int gsa_topk_select_adaptive(const float* scores, int64_t s_sb, int64_t s_st,
  * gsa_indexer_select_workspace_bytes(B, T) bytes (16-byte aligned),
  * overwritten by each call: the causal score tiles, stored once and read
  * back instead of recomputed (B * G(G+1)/2 KiB, G = ceil(T/16)), and the
- * threshold candidates of each 16-row group (B * G * 64 KiB).
+ * threshold candidates of each 16-row group (B * G * 128 KiB).
  * Supported: Hi == 4, di == 64, 1 <= k_eff <= T.
  */
 size_t gsa_indexer_select_workspace_bytes(int B, int T);

@@ -76,7 +76,7 @@ def test_indexer_scores_validation(lib):
     assert _scores(lib, qst=260) == 4        # row stride not a multiple of 8 bf16
 
 
-NWS_T32 = 3 * 1024 + 2 * 16 * 512 * 8    # indexer-select workspace at B=1, T=32
+NWS_T32 = 3 * 1024 + 2 * 16 * 1024 * 8    # indexer-select workspace at B=1, T=32
 
 
 def _select(lib, **kw):
@@ -103,8 +103,8 @@ def test_indexer_select_validation(lib):
     assert _select(lib, nws=NWS_T32 - 1) == 2     # workspace too small
     assert _select(lib, ws=P + 8) == 4
     # one 1 KiB score tile per causal (16-row group, 16-key tile) pair, then
-    # 16 rows x 512 (key, index) candidate slots of 8 bytes per 16-row group
-    cand = 16 * 512 * 8
+    # 16 rows x 1024 (key, index) candidate slots of 8 bytes per 16-row group
+    cand = 16 * 1024 * 8
     assert lib.gsa_indexer_select_workspace_bytes(1, 32) == NWS_T32 == 3 * 1024 + 2 * cand
     assert lib.gsa_indexer_select_workspace_bytes(2, 100) == 2 * (28 * 1024 + 7 * cand)
     assert lib.gsa_indexer_select_workspace_bytes(1, 65536) == 4096 * 4097 // 2 * 1024 + 4096 * cand
