@@ -142,6 +142,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--k-mode", choices=["fixed", "variance"], default="fixed",
                     help="selector: fixed k_eff (the reference) or the variance-based per-row k")
+    ap.add_argument("--proj", choices=["gemm", "fused"], default="gemm",
+                    help="main projection: hipBLASLt GEMM + producer kernel, or the fused MFMA GEMM "
+                         "with the producer in its epilogue")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after timing, run one plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -154,11 +157,14 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
 
+    from gsa_gdn_benchmarkstudy_amd import _abi
+
     dev = torch.device("cuda:0")
     B, T = CONFIGS[args.config]
     dtype = torch.bfloat16
     model = synthetic_model(dev, dtype)
     model.topk_selector.mode = args.k_mode
+    model.proj_impl = args.proj
     g = torch.Generator(device="cpu").manual_seed(1)
     x = torch.randn(B, T, D, generator=g)
     if args.config == "c4":   # per-sequence sigma ~ U(0.5, 2)
@@ -223,6 +229,31 @@ def main():
         idx_ms = e0.elapsed_time(e1) / n_idx
         del views
 
+    # the main projection and its producer both ways (hipBLASLt GEMM + producer
+    # kernel; fused MFMA GEMM with the producer in its epilogue), timed alone
+    proj = {"impl": args.proj}
+    with torch.no_grad():
+        cos, sin = model.rotary_emb(T, dev, dtype)
+        cos, sin = cos.contiguous(), sin.contiguous()
+
+        def unfused():
+            v = model.project_main(x)
+            return _abi.prologue_vt(v["v"], v["vg"], k=v["k"], cos=cos, sin=sin)
+
+        ways = {"gemm_producer_ms": unfused}
+        if _abi.proj_supported(D, H, T):
+            ways["fused_ms"] = lambda: model.project_fused(x, cos, sin)
+        for name, fn in ways.items():
+            fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            proj[name] = e0.elapsed_time(e1) / 5
+
     if args.calib_copy_mib:
         n = args.calib_copy_mib * (1 << 20) // 4
         src = torch.ones(n, device=dev, dtype=torch.float32)
@@ -273,13 +304,14 @@ def main():
                                + (f"k_eff={k_eff}" if args.k_mode == "fixed" else
                                   f"variance-adaptive k (k_base={K_BASE}, k_min={K_MIN}, k_max={K_MAX})")
                                + " causal", "name": args.config, "batch": B, "seq_len": T,
-                   "k_mode": args.k_mode, "k_eff": k_eff if args.k_mode == "fixed" else k_stats},
+                   "proj": args.proj, "k_mode": args.k_mode, "k_eff": k_eff if args.k_mode == "fixed" else k_stats},
         "roofline": roofline,
         "gather_attention": gather_roof,
         "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,
                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": idx_tflops / BF16_PEAK_TFLOPS,
                     "traffic": profiled_traffic("gsa_indexer_select", args.config),
                     "flops": fidx, "ms": idx_ms},
+        "projection": proj,
         "peak_mem_gib": peak_mem / 2**30,
     }
     if not args.no_cpu_baseline:

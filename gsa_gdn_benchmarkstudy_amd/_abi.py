@@ -36,6 +36,7 @@ EXPORTS = (
     "gsa_selection_mask", "gsa_dense_attn", "gsa_dense_attn_workspace_bytes",
     "gsa_indexer_select_workspace_bytes", "gsa_indexer_select_adaptive",
     "gsa_indexer_select_adaptive_workspace_bytes", "gsa_topk_select_adaptive",
+    "gsa_proj_packed_bytes", "gsa_proj_pack", "gsa_proj_fused",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -69,6 +70,10 @@ _PROTOS = {
                         _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64,
                         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_dense_attn_workspace_bytes": ([_i32, _i32, _i32], ctypes.c_size_t),
+    "gsa_proj_packed_bytes": ([_i32, _i32], ctypes.c_size_t),
+    "gsa_proj_pack": ([_vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
+    "gsa_proj_fused": ([_vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64,
+                        _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], _i32),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -424,6 +429,68 @@ def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None):
                              _stream(v))
     _check(st, "gsa_prologue_vt")
     return k_out, vt
+
+
+def proj_supported(D: int, H: int, T: int) -> bool:
+    """Shapes the fused projection kernel takes: d_head 128, an even head count, T % 64 == 0."""
+    return H >= 2 and H <= 64 and D == 128 * H and D % 256 == 0 and T % 64 == 0
+
+
+def proj_pack(w, bias=None):
+    """Packed weight (bf16, flat) and fp32 bias of the fused projection from the q, k, v,
+    value-gate and output-gate rows ``w`` [5D, D] (row stride may exceed D) and their bias [5D]."""
+    lib = load()
+    _need_cuda(w, bias)
+    n, D = w.shape
+    _expect(n == 5 * D and w.dtype == torch.bfloat16 and w.stride(1) == 1, "w: bf16 [5D, D] with unit column stride")
+    H = D // 128
+    nbytes = lib.gsa_proj_packed_bytes(D, H)
+    _expect(nbytes > 0, f"fused projection: D={D} unsupported (needs D = 128*H, D % 256 == 0)")
+    if bias is not None:
+        _expect(bias.dim() == 1 and bias.shape[0] >= n and bias.dtype == w.dtype and bias.stride(0) == 1,
+                "bias: bf16 [>=5D]")
+    wp = torch.empty(nbytes // 2, device=w.device, dtype=torch.bfloat16)
+    bp = torch.empty(n, device=w.device, dtype=torch.float32)
+    st = lib.gsa_proj_pack(_ptr(w), w.stride(0), _ptr(bias), D, H, DTYPE_BF16, _ptr(wp), _ptr(bp), _stream(w))
+    _check(st, "gsa_proj_pack")
+    return wp, bp
+
+
+def proj_fused(x, wp, bp, cos, sin, H: int, q=None, og=None, k_out=None, vt=None):
+    """x [B,T,D] -> q, og (bf16 [B,T,H,128] views of one [B,T,2,D] buffer unless given),
+    RoPE(k) [B,T,H,128] and (v*sigmoid(vg))^T [B,H,128,ldv], from the packed projection."""
+    lib = load()
+    _need_cuda(x, wp, bp, cos, sin)
+    B, T, D = x.shape
+    _expect(x.dtype == torch.bfloat16 and x.stride(2) == 1 and x.stride(0) == T * x.stride(1),
+            "x: bf16 [B,T,D] with uniformly strided rows")
+    _expect(proj_supported(D, H, T), f"fused projection: D={D} H={H} T={T} unsupported")
+    _expect(wp.numel() * 2 == lib.gsa_proj_packed_bytes(D, H) and bp.numel() == 5 * D and bp.dtype == torch.float32,
+            "wp/bp: from proj_pack for this D")
+    _expect(cos.dim() == 2 and cos.shape[0] >= T and cos.shape[1] == 128 and tuple(sin.shape) == tuple(cos.shape)
+            and cos.dtype == sin.dtype == x.dtype and cos.stride(1) == 1 and sin.stride() == cos.stride(),
+            "cos/sin: [>=T, 128] bf16")
+    dev, dt = x.device, x.dtype
+    if q is None or og is None:
+        qo = torch.empty(B, T, 2, H, 128, device=dev, dtype=dt)
+        q, og = qo[:, :, 0], qo[:, :, 1]
+    for t, nm in ((q, "q"), (og, "og")):
+        _expect(tuple(t.shape) == (B, T, H, 128) and t.dtype == dt and t.stride(3) == 1 and t.stride(2) == 128
+                and t.stride(0) == T * t.stride(1), f"{nm}: [B,T,H,128] with uniformly strided rows")
+    if k_out is None:
+        k_out = torch.empty(B, T, H, 128, device=dev, dtype=dt)
+    _expect(tuple(k_out.shape) == (B, T, H, 128) and k_out.is_contiguous() and k_out.dtype == dt,
+            "k_out: contiguous [B,T,H,128]")
+    ldv = vt_len(T)
+    if vt is None:
+        vt = torch.empty(B, H, 128, ldv, device=dev, dtype=dt)
+    _expect(tuple(vt.shape) == (B, H, 128, ldv) and vt.is_contiguous() and vt.dtype == dt,
+            "vt: contiguous [B,H,128,ldv]")
+    st = lib.gsa_proj_fused(_ptr(x), x.stride(1), B, T, D, H, DTYPE_BF16, _ptr(wp), _ptr(bp), _ptr(cos),
+                            _ptr(sin), cos.stride(0), _ptr(q), q.stride(1), _ptr(og), og.stride(1),
+                            _ptr(k_out), _ptr(vt), ldv, _stream(x))
+    _check(st, "gsa_proj_fused")
+    return q, og, k_out, vt
 
 
 def selection_mask(idx, Tkv: int, count=None, mask=None, out=None):

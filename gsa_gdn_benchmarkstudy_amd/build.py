@@ -19,7 +19,7 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libgsa_hip.so")
 ARCH = "gfx950"
 
-HIP_SOURCES = ("indexer.hip", "topk_select.hip", "sparse_attn.hip", "dense_attn.hip")
+HIP_SOURCES = ("indexer.hip", "topk_select.hip", "sparse_attn.hip", "dense_attn.hip", "proj_fused.hip")
 CXX_SOURCES = ("abi.cpp",)
 
 # Packed fp32 VALU forms are disabled in device code: the compiler would

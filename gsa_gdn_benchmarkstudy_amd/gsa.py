@@ -325,6 +325,7 @@ class GatedSparseAttention(nn.Module):
 
         self._fused_weight: Optional[torch.Tensor] = None
         self._fused_bias: Optional[torch.Tensor] = None
+        self._packed: Optional[tuple] = None
         self._idx_bias32: Optional[torch.Tensor] = None
         self._proj_sizes = [
             hidden_size, hidden_size, hidden_size, hidden_size, hidden_size,
@@ -344,6 +345,11 @@ class GatedSparseAttention(nn.Module):
         # indexer's grid (one block per 16 query rows) leaves CUs free for the
         # GEMM -- fewer than 4 blocks per CU -- else "producer".
         self.indexer_overlap = "auto"
+        # Main projection on the bf16 block-dense path: "gemm" (hipBLASLt GEMM,
+        # then the RoPE / value-gate producer kernel) or "fused" (own MFMA GEMM
+        # with that producer in its epilogue; needs an even head count and
+        # T % 64 == 0, else "gemm" runs).
+        self.proj_impl = "gemm"
         # Optional per-kernel timing hook: a list to which forward appends
         # (start, end) event pairs around the sparse-attention launch.
         self.attn_events: Optional[list] = None
@@ -353,6 +359,7 @@ class GatedSparseAttention(nn.Module):
     def _drop_fused(self) -> None:
         self._fused_weight = None
         self._fused_bias = None
+        self._packed = None
         self._idx_bias32 = None
 
     def fuse_projections(self) -> None:
@@ -374,6 +381,7 @@ class GatedSparseAttention(nn.Module):
         bias[off["iw"]:off["iw"] + self.indexer.n_idx_heads] = self.indexer.idx_w_proj.bias.detach()
         self._fused_weight = w.contiguous()
         self._fused_bias = bias
+        self._packed = None
         # fp32 copy of the indexer bias for the kernels (built here, not per call)
         self._idx_bias32 = self.indexer.idx_bias.detach().float().contiguous()
 
@@ -416,6 +424,24 @@ class GatedSparseAttention(nn.Module):
         v = {n: comb[..., off[n]:off[n] + D].view(B, T, H, d) for n in ("q", "k", "v", "vg", "og")}
         v["_buf"] = comb
         return v
+
+    def uses_fused_projection(self, x: torch.Tensor) -> bool:
+        if self.proj_impl not in ("gemm", "fused"):
+            raise ValueError(f"proj_impl {self.proj_impl!r}: expected 'gemm' or 'fused'")
+        B, T, D = x.shape
+        return (self.proj_impl == "fused" and self.uses_dense(x.dtype)
+                and _abi.proj_supported(D, self.num_heads, T) and self.d_head == 128)
+
+    def project_fused(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+        """Main projection with the producer fused (gsa_proj_fused) -> dict with the raw q
+        and og views, RoPE(k) and V^T = (v*sigmoid(vg))^T."""
+        w, b = self._get_fused_weight(x)
+        D = self.hidden_size
+        if self._packed is None or self._packed[0].device != x.device:
+            self._packed = _abi.proj_pack(w[:5 * D], b[:5 * D])
+        wp, bp = self._packed
+        q, og, k_rope, vt = _abi.proj_fused(x, wp, bp, cos, sin, self.num_heads)
+        return {"q": q, "og": og, "_k_rope": k_rope, "_vt": vt}
 
     def project(self, x: torch.Tensor):
         """All eight projections -> dict of strided [B,T,...] views."""
@@ -464,6 +490,14 @@ class GatedSparseAttention(nn.Module):
         cur = torch.cuda.current_stream(dev)
 
         dense = self.uses_dense(x.dtype)
+        fused_proj = self.uses_fused_projection(x)
+        cos, sin = self.rotary_emb(T, dev, x.dtype)
+        cos, sin = cos.contiguous(), sin.contiguous()
+
+        def main_projection():
+            if fused_proj:
+                return self.project_fused(x, cos, sin)
+            return self.project_main(x)
 
         # Track A: the indexer projections, then the fused indexer + top-k
         # (and its bitmask), on a side stream that starts after the main
@@ -488,7 +522,7 @@ class GatedSparseAttention(nn.Module):
             side = self._indexer_stream
         if mode == "producer":
             _range_push("gsa_hip/main_gemm")
-            views.update(self.project_main(x))
+            views.update(main_projection())
             _range_pop()
         if side is not cur:
             side.wait_stream(cur)
@@ -498,14 +532,14 @@ class GatedSparseAttention(nn.Module):
             _range_pop()
         if mode != "producer":
             _range_push("gsa_hip/main_gemm")
-            views.update(self.project_main(x))
+            views.update(main_projection())
             _range_pop()
 
         # Track B: RoPE(k) and the value gate on the current stream
         _range_push("gsa_hip/prologue")
-        cos, sin = self.rotary_emb(T, dev, x.dtype)
-        cos, sin = cos.contiguous(), sin.contiguous()
-        if dense:
+        if fused_proj:
+            k_rope, v_gated = views["_k_rope"], views["_vt"]
+        elif dense:
             k_rope, v_gated = _abi.prologue_vt(views["v"], views["vg"], k=views["k"], cos=cos, sin=sin)
         else:
             k_rope, v_gated = _abi.prologue(k=views["k"], v=views["v"], vg=views["vg"], cos=cos, sin=sin)

@@ -283,6 +283,41 @@ int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                    void* ws, size_t ws_bytes,
                    void* stream);
 
+/*
+ * Main projection GEMM with the producer fused into its epilogue.
+ * Replaces the phase-1 projection GEMM and its split (gsa_triton/gsa_opt.py:
+ * 629-638) together with the track-B producer steps that follow it: the
+ * value gate v*sigmoid(vg) (gsa_opt.py:685-690) and RoPE(k) (gsa_opt.py:
+ * 692-697) -- the producer fusion listed as future work in
+ * gsa_triton/README.md:424-433.  RoPE(q) and the output gate stay in
+ * gsa_dense_attn, which consumes every output here.
+ *
+ * gsa_proj_pack (once per weight update): w [5D, D] bf16 (row stride w_st)
+ * holds the q, k, v, value-gate and output-gate projection rows in that
+ * order, bias [5D] bf16 or NULL (zeros); writes the permuted, tiled weight
+ * w_packed (gsa_proj_packed_bytes(D, H) bytes, 16-byte aligned) and the
+ * fp32 bias bias_packed [5D].  Supported: D == 128*H, D % 256 == 0 (even H).
+ *
+ * gsa_proj_fused: x [B*T, D] bf16 rows (stride x_st, multiple of 8) ->
+ *   q  [B*T, D] rows (stride q_st):  bf16(x W_q^T + b_q)
+ *   og [B*T, D] rows (stride og_st): bf16(x W_og^T + b_og)
+ *   k_out [B,T,H,128] contiguous:    RoPE(bf16(x W_k^T + b_k)) with cos/sin
+ *                                    [>=T, 128] bf16 (row stride cs_st)
+ *   vt [B,H,128,ldv] contiguous:     (bf16(x W_v^T + b_v) *
+ *                                    bf16(sigmoid(bf16(x W_vg^T + b_vg))))^T,
+ *                                    keys [T, ldv) zero
+ * with the rounding points of the unfused path (projection rounded to bf16,
+ * then gsa_prologue_vt's steps).  Needs T % 64 == 0, ldv >= T, ldv % 64 == 0.
+ */
+size_t gsa_proj_packed_bytes(int D, int H);
+int gsa_proj_pack(const void* w, int64_t w_st, const void* bias, int D, int H, int dtype,
+                  void* w_packed, float* bias_packed, void* stream);
+int gsa_proj_fused(const void* x, int64_t x_st, int B, int T, int D, int H, int dtype,
+                   const void* w_packed, const float* bias_packed,
+                   const void* cos, const void* sin, int64_t cs_st,
+                   void* q, int64_t q_st, void* og, int64_t og_st,
+                   void* k_out, void* vt, int ldv, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

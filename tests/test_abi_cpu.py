@@ -251,3 +251,38 @@ def test_sparse_attn_validation(lib):
     assert call(ksel=-1) == 5
     assert call(q=MIS) == 4
     assert call(idx=P + 2) == 4
+
+
+def test_proj_validation(lib):
+    assert lib.gsa_proj_packed_bytes(2048, 16) == 5 * 2048 * 2048 * 2
+    assert lib.gsa_proj_packed_bytes(256, 2) == 5 * 256 * 256 * 2
+    assert lib.gsa_proj_packed_bytes(384, 3) == 0          # odd head count: no 256-column tiles
+    assert lib.gsa_proj_packed_bytes(2048, 8) == 0         # d_head != 128
+    pk = lib.gsa_proj_pack
+    assert pk(None, 2048, None, 2048, 16, 1, P, P, None) == 1
+    assert pk(P, 2048, None, 2048, 16, 0, P, P, None) == 3
+    assert pk(P, 2048, None, 384, 3, 1, P, P, None) == 2
+    assert pk(P, 1000, None, 2048, 16, 1, P, P, None) == 2   # row stride < D
+    assert pk(MIS, 2048, None, 2048, 16, 1, P, P, None) == 4
+    f = lib.gsa_proj_fused
+    ok = dict(x=P, xst=2048, B=1, T=512, D=2048, H=16, dtype=1, wp=P, bp=P, cos=P, sin=P, cst=128,
+              q=P, qst=4096, og=P, ogst=4096, ko=P, vt=P, ldv=512)
+
+    def call(**kw):
+        a = dict(ok)
+        a.update(kw)
+        return f(a["x"], a["xst"], a["B"], a["T"], a["D"], a["H"], a["dtype"], a["wp"], a["bp"], a["cos"],
+                 a["sin"], a["cst"], a["q"], a["qst"], a["og"], a["ogst"], a["ko"], a["vt"], a["ldv"], None)
+
+    assert call(x=None) == 1
+    assert call(vt=None) == 1
+    assert call(dtype=0) == 3
+    assert call(T=100) == 2                       # T % 64
+    assert call(D=384, H=3) == 2
+    assert call(ldv=448) == 2                     # ldv < T
+    assert call(ldv=576 + 8) == 2                 # ldv % 64
+    assert call(xst=1000) == 2                    # row stride < D
+    assert call(x=MIS) == 4
+    assert call(xst=2052) == 4                    # rows not 16-byte aligned
+    assert call(qst=4098) == 4
+    assert call(cst=130) == 4
