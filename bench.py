@@ -145,6 +145,8 @@ def main():
     ap.add_argument("--proj", choices=["gemm", "fused"], default="gemm",
                     help="main projection: hipBLASLt GEMM + producer kernel, or the fused MFMA GEMM "
                          "with the producer in its epilogue")
+    ap.add_argument("--graph", action="store_true",
+                    help="time HIP-graph replays of the forward (one launch per step)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after timing, run one plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -177,13 +179,27 @@ def main():
             model(x)
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats(dev)
-        model.attn_events = []
+        step = (lambda: model(x))
+        if args.graph:
+            from gsa_gdn_benchmarkstudy_amd.graph import GraphedForward
+            graphed = GraphedForward(model, x, warmup=1)
+            step = (lambda: graphed(x))
+            for _ in range(args.warmup):
+                step()
+            torch.cuda.synchronize()
+        else:
+            model.attn_events = []
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(args.steps):
-            model(x)
+            step()
         end.record()
         torch.cuda.synchronize()
+        if args.graph:      # the attention kernel's own time from eager forwards
+            model.attn_events = []
+            for _ in range(min(args.steps, 5)):
+                model(x)
+            torch.cuda.synchronize()
         evs = model.attn_events
         model.attn_events = None
     total_ms = start.elapsed_time(end)
@@ -304,7 +320,7 @@ def main():
                                + (f"k_eff={k_eff}" if args.k_mode == "fixed" else
                                   f"variance-adaptive k (k_base={K_BASE}, k_min={K_MIN}, k_max={K_MAX})")
                                + " causal", "name": args.config, "batch": B, "seq_len": T,
-                   "proj": args.proj, "k_mode": args.k_mode, "k_eff": k_eff if args.k_mode == "fixed" else k_stats},
+                   "proj": args.proj, "graph": args.graph, "k_mode": args.k_mode, "k_eff": k_eff if args.k_mode == "fixed" else k_stats},
         "roofline": roofline,
         "gather_attention": gather_roof,
         "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,

@@ -256,9 +256,12 @@ def format_row(r: Row) -> str:
 
 def sweep(cls, label: str, points: Sequence[Tuple[int, int, int]], device, dtype: torch.dtype,
           warmup: int = WARMUP_ITERS, iters: int = BENCH_ITERS, attn_impl: Optional[str] = None,
-          seed: int = 0, timer: Callable = event_timer,
+          seed: int = 0, timer: Callable = event_timer, graph: bool = False,
           out: Callable[[str], None] = print) -> List[Row]:
-    """Time ``cls`` at every (B, T, D) point (gsa_triton/benchmark.py:150-222)."""
+    """Time ``cls`` at every (B, T, D) point (gsa_triton/benchmark.py:150-222).
+
+    graph: time replays of a HIP graph of the forward (GraphedForward) instead of
+    eager forwards (this build's layer only)."""
     out(f"\n{'=' * 60}\n  {label}\n{'=' * 60}")
     out(f"{'B':<5} {'T':<7} {'D':<6} | {'ms':>9} | {'tok/s':>14} | {'MB':>9}")
     out("-" * 60)
@@ -275,7 +278,13 @@ def sweep(cls, label: str, points: Sequence[Tuple[int, int, int]], device, dtype
             with torch.no_grad():
                 for _ in range(warmup):
                     model(x)
-                ms = timer(lambda: model(x), iters, device)
+                fn = (lambda: model(x))
+                if graph:
+                    from .graph import GraphedForward
+                    fn = GraphedForward(model, x, warmup=1)
+                    fx = fn
+                    fn = (lambda: fx(x))
+                ms = timer(fn, iters, device)
             row.ms, row.tok_per_s, row.mem_mb = ms, B * T / (ms / 1e3), _peak_mb(device)
         except Exception as exc:  # every failure becomes a row; the sweep goes on
             row.status = classify_failure(exc)
@@ -405,6 +414,8 @@ def parse_args(argv: Optional[Sequence[str]] = None) -> argparse.Namespace:
     p.add_argument("--iters", type=int, default=BENCH_ITERS)
     p.add_argument("--attn", choices=["auto", "dense", "gather"], default="auto",
                    help="attention kernel of this build's layer")
+    p.add_argument("--graph", action="store_true",
+                   help="time HIP-graph replays of this build's forward (one launch per forward)")
     p.add_argument("--json", default=None, help="also write the results to this JSON file")
     # capture windows: the reference's --profile / --ncu flags, same names
     p.add_argument("--profile", action="store_true",
@@ -472,7 +483,8 @@ def main(argv: Optional[Sequence[str]] = None, out: Callable[[str], None] = prin
         capture(r, o, device, dtype, B, T, iters, tag, warmup=a.warmup, attn_impl=attn, out=out)
         return 0
 
-    report: Dict[str, object] = {"device": torch.cuda.get_device_name(device), "dtype": a.dtype}
+    report: Dict[str, object] = {"device": torch.cuda.get_device_name(device), "dtype": a.dtype,
+                                 "graph": a.graph}
     if a.skip_verify:
         report["verify"] = "skipped"
     elif ref_cls is None:
@@ -494,8 +506,8 @@ def main(argv: Optional[Sequence[str]] = None, out: Callable[[str], None] = prin
     if ref_cls is not None:
         ref_rows = sweep(ref_cls, "reference layer (--ref)", points, device, dtype,
                          warmup=a.warmup, iters=a.iters, out=out)
-    opt_rows = sweep(opt_cls, "gsa_hip (MI355X HIP kernels)", points, device, dtype,
-                     warmup=a.warmup, iters=a.iters, attn_impl=attn, out=out)
+    opt_rows = sweep(opt_cls, "gsa_hip (MI355X HIP kernels)" + (", HIP graph" if a.graph else ""), points,
+                     device, dtype, warmup=a.warmup, iters=a.iters, attn_impl=attn, graph=a.graph, out=out)
     if ref_rows:
         for line in summary_lines(ref_rows, opt_rows):
             out(line)

@@ -76,3 +76,14 @@ def test_harness_main_verifies_and_summarises(dev, tmp_path):
 def test_harness_capture_modes(dev, flags):
     _log(f"harness main {' '.join(flags)}")
     assert harness.main(flags + ["--warmup", "1"], out=_log) == 0
+
+
+def test_harness_sweep_graph(dev, tmp_path):
+    path = tmp_path / "graph.json"
+    _log("harness main --skip-verify --graph --T 512,1024")
+    rc = harness.main(["--skip-verify", "--graph", "--T", "512,1024", "--warmup", "1", "--iters", "3",
+                       "--json", str(path)], out=_log)
+    assert rc == 0
+    rep = json.loads(path.read_text())
+    assert rep["graph"] is True
+    assert [r["status"] for r in rep["opt"]] == ["ok", "ok"]
