@@ -342,7 +342,11 @@ def _dense_case(B, T, H, k, seed):
     return q, kk, v, og, ia, cnt
 
 
-@pytest.mark.parametrize("B,T,H,k", [(1, 64, 16, 16), (2, 100, 4, 37), (1, 300, 2, 100), (1, 1030, 16, 256)])
+@pytest.mark.parametrize("B,T,H,k", [(1, 64, 16, 16), (2, 100, 4, 37), (1, 300, 2, 100), (1, 1030, 16, 256),
+                                     # 256-row query blocks and 64-key tiles: one short of, at and
+                                     # one past the boundaries; one head; odd batch counts
+                                     (1, 255, 1, 64), (3, 256, 2, 32), (1, 257, 1, 256), (2, 513, 2, 100),
+                                     (1, 767, 3, 767)])
 def test_dense_attention_vs_oracle_and_gather(dev, B, T, H, k):
     _log(f"dense_attn B={B} T={T} H={H} k={k}")
     q, kk, v, og, ia, cnt = _dense_case(B, T, H, k, seed=T + H)
