@@ -456,7 +456,11 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
   // loads and any such wait would drain them.
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
-  floatx16 sc0 = s_half(0, 0), sc1 = s_half(0, 1);   // S^T of tile 0
+  // S^T of tile kt in sc[kt & 1]: with the loop unrolled by two, each
+  // iteration writes the other pair, so no accumulator is copied
+  floatx16 sc[2][2];
+  sc[0][0] = s_half(0, 0);
+  sc[0][1] = s_half(0, 1);                          // S^T of tile 0
 
   const char* ksrc = kbase + 2 * kstep;              // K tile kt+2
   const char* vsrc = vtb + kDK * 2;                  // V^T tile kt+1
@@ -475,16 +479,14 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
 
     uint32_t pk0[2][4], pk1[2][4];
     float alpha0, alpha1;
-    const floatx16 n0 = s_half(1 - P, 0);          // S^T(kt+1) || softmax(kt); stale on the last tile, unused
-    const bool bump0 = softmax_half(sc0, lmt, 0, pk0, alpha0);
-    const floatx16 n1 = s_half(1 - P, 1);
-    const bool bump1 = softmax_half(sc1, lmt, 1, pk1, alpha1);
+    sc[1 - P][0] = s_half(1 - P, 0);               // S^T(kt+1) || softmax(kt); stale on the last tile, unused
+    const bool bump0 = softmax_half(sc[P][0], lmt, 0, pk0, alpha0);
+    sc[1 - P][1] = s_half(1 - P, 1);
+    const bool bump1 = softmax_half(sc[P][1], lmt, 1, pk1, alpha1);
     if (ballot64(bump0)) rescale(alpha0);
     pv_half(P, 0, pk0);
     if (ballot64(bump1)) rescale(alpha1);
     pv_half(P, 1, pk1);
-    sc0 = n0;
-    sc1 = n1;
     lmt += 32;
   };
   int kt = 0;
