@@ -238,11 +238,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
 // compiler's own bookkeeping does not make each LDS read wait for every such
 // load in flight; completion is awaited explicitly (vmcnt) before the
 // barrier that publishes a tile.  m0 holds the LDS address; nothing else in
-// this kernel uses m0.
+// this kernel uses m0.  An LDS DMA reads m0 one wait state after the SALU
+// write at the earliest (the s_nop; the compiler pads its own LDS DMA the
+// same way on gfx950).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void load_lds16(const void* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop

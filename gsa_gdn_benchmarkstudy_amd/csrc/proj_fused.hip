@@ -98,9 +98,10 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint16_t* __restrict__ 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 // Direct global -> LDS load: each lane's 16 bytes at base + voff land at
-// lds + 16 * lane.  Completion is awaited with explicit vmcnt waits.
+// lds + 16 * lane.  Completion is awaited with explicit vmcnt waits.  The
+// s_nop is the wait state an LDS DMA needs after the SALU write of m0.
 __device__ __forceinline__ void load_lds16(const void* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
