@@ -145,6 +145,8 @@ def main():
     ap.add_argument("--proj", choices=["gemm", "fused"], default="gemm",
                     help="main projection: hipBLASLt GEMM + producer kernel, or the fused MFMA GEMM "
                          "with the producer in its epilogue")
+    ap.add_argument("--overlap", choices=["auto", "producer", "gemm", "serial"], default="auto",
+                    help="where the indexer runs relative to the projection GEMM and the producer")
     ap.add_argument("--graph", action="store_true",
                     help="time HIP-graph replays of the forward (one launch per step)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -167,6 +169,7 @@ def main():
     model = synthetic_model(dev, dtype)
     model.topk_selector.mode = args.k_mode
     model.proj_impl = args.proj
+    model.indexer_overlap = args.overlap
     g = torch.Generator(device="cpu").manual_seed(1)
     x = torch.randn(B, T, D, generator=g)
     if args.config == "c4":   # per-sequence sigma ~ U(0.5, 2)
@@ -320,7 +323,7 @@ def main():
                                + (f"k_eff={k_eff}" if args.k_mode == "fixed" else
                                   f"variance-adaptive k (k_base={K_BASE}, k_min={K_MIN}, k_max={K_MAX})")
                                + " causal", "name": args.config, "batch": B, "seq_len": T,
-                   "proj": args.proj, "graph": args.graph, "k_mode": args.k_mode, "k_eff": k_eff if args.k_mode == "fixed" else k_stats},
+                   "proj": args.proj, "overlap": args.overlap, "graph": args.graph, "k_mode": args.k_mode, "k_eff": k_eff if args.k_mode == "fixed" else k_stats},
         "roofline": roofline,
         "gather_attention": gather_roof,
         "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,

@@ -34,6 +34,8 @@ FUSED_ALIGN = 64
 
 
 _CU_COUNT = {}
+# Last-level (Infinity) cache of one MI355X.
+_LLC_BYTES = 256 << 20
 
 
 def _cu_count(dev: torch.device) -> int:
@@ -343,7 +345,10 @@ class GatedSparseAttention(nn.Module):
         # the GEMM, on a side stream beside the RoPE/gate producer), "serial"
         # (everything on the current stream) or "auto": "gemm" while the
         # indexer's grid (one block per 16 query rows) leaves CUs free for the
-        # GEMM -- fewer than 4 blocks per CU -- else "producer".
+        # GEMM -- fewer than 4 blocks per CU; else "serial" while RoPE(k) and
+        # V^T together fit the 256 MB last-level cache (the producer then
+        # runs right before the attention, which finds them cached); else
+        # "producer".
         self.indexer_overlap = "auto"
         # Main projection on the bf16 block-dense path: "gemm" (hipBLASLt GEMM,
         # then the RoPE / value-gate producer kernel) or "fused" (own MFMA GEMM
@@ -503,12 +508,19 @@ class GatedSparseAttention(nn.Module):
         # (and its bitmask), on a side stream that starts after the main
         # projection GEMM ("producer"), right after the small indexer GEMM
         # ("gemm"), or on the current stream ("serial").  The indexer and the
-        # GEMM both fill the GPU and slow each other down when they share it;
-        # beside the HBM-bound producer the indexer's light tail blocks leave
-        # room for it.
+        # GEMM both fill the GPU and slow each other down when they share it.
+        # Serially, the producer runs last before the attention and its
+        # outputs (RoPE(k), V^T: 2*B*T*D elements) are still in the MI355X's
+        # 256 MB last-level cache when the attention streams them; beyond
+        # that size the producer is better hidden beside the indexer.
         mode = self.indexer_overlap
         if mode == "auto":
-            mode = "gemm" if B * ((T + 15) // 16) < 4 * _cu_count(dev) else "producer"
+            if B * ((T + 15) // 16) < 4 * _cu_count(dev):
+                mode = "gemm"
+            elif 2 * B * T * D * x.element_size() <= _LLC_BYTES:
+                mode = "serial"
+            else:
+                mode = "producer"
         elif mode not in ("producer", "gemm", "serial"):
             raise ValueError(f"indexer_overlap {mode!r}: expected 'auto', 'producer', 'gemm' or 'serial'")
         _range_push("gsa_hip/indexer_gemm")
