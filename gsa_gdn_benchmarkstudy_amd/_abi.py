@@ -28,6 +28,7 @@ TOPK_DESC_MAX_K = 4096
 
 ATTN_ROPE_Q = 1
 ATTN_OUT_GATE = 2
+ATTN_MASKS_READY = 4
 
 # Every symbol include/gsa_hip.h declares.
 EXPORTS = (
@@ -36,7 +37,7 @@ EXPORTS = (
     "gsa_selection_mask", "gsa_dense_attn", "gsa_dense_attn_workspace_bytes",
     "gsa_indexer_select_workspace_bytes", "gsa_indexer_select_adaptive",
     "gsa_indexer_select_adaptive_workspace_bytes", "gsa_topk_select_adaptive",
-    "gsa_proj_packed_bytes", "gsa_proj_pack", "gsa_proj_fused",
+    "gsa_proj_packed_bytes", "gsa_proj_pack", "gsa_proj_fused", "gsa_dense_lane_masks",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -71,6 +72,7 @@ _PROTOS = {
                         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_dense_attn_workspace_bytes": ([_i32, _i32, _i32], ctypes.c_size_t),
     "gsa_proj_packed_bytes": ([_i32, _i32], ctypes.c_size_t),
+    "gsa_dense_lane_masks": ([_vp, _i64, _i64, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_proj_pack": ([_vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
     "gsa_proj_fused": ([_vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64,
                         _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], _i32),
@@ -514,11 +516,29 @@ def selection_mask(idx, Tkv: int, count=None, mask=None, out=None):
     return out
 
 
+def dense_lane_masks(bits, Tkv: int, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Lane masks of the dense attention from the selection bitmask [B,T,W] -> the
+    workspace tensor holding them (pass it to dense_attn with masks_ready=True)."""
+    lib = load()
+    _need_cuda(bits, ws)
+    B, T, W = bits.shape
+    _expect(W == mask_words(Tkv) and bits.stride(2) == 1 and bits.dtype == torch.int32, "bits: int32 [B,T,W]")
+    nbytes = lib.gsa_dense_attn_workspace_bytes(B, T, Tkv)
+    if ws is None:
+        ws = torch.empty(nbytes, device=bits.device, dtype=torch.uint8)
+    _expect(ws.numel() * ws.element_size() >= nbytes and ws.is_contiguous(), "workspace too small")
+    st = lib.gsa_dense_lane_masks(_ptr(bits), bits.stride(0), bits.stride(1), B, T, Tkv, _ptr(ws), nbytes,
+                                  _stream(bits))
+    _check(st, "gsa_dense_lane_masks")
+    return ws
+
+
 def dense_attn(q, k, vt, bits, scale: float, og=None, cos=None, sin=None, flags: int = 0,
                causal: bool = True, out: Optional[torch.Tensor] = None,
-               ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+               ws: Optional[torch.Tensor] = None, masks_ready: bool = False) -> torch.Tensor:
     """Block-dense masked attention -> out [B,T,H,d] (bf16).  ``ws``: optional
-    workspace (uint8 device tensor of at least dense_attn_workspace_bytes)."""
+    workspace (uint8 device tensor of at least dense_attn_workspace_bytes);
+    ``masks_ready``: ws already holds dense_lane_masks(bits) (bits is then not read)."""
     lib = load()
     _need_cuda(q, k, vt, bits, og, cos, sin)
     B, T, H, d = q.shape
@@ -529,6 +549,7 @@ def dense_attn(q, k, vt, bits, scale: float, og=None, cos=None, sin=None, flags:
             and vt.stride(3) == 1 and vt.stride(2) == vt.shape[3] and vt.dtype == q.dtype,
             "vt: [B,H,d,ldv] rows of ldv >= Tkv rounded up to 64")
     _expect(tuple(bits.shape) == (B, T, mask_words(Tkv)) and bits.stride(2) == 1, "bits: [B,T,W]")
+    _expect(not masks_ready or ws is not None, "masks_ready needs the workspace that holds the masks")
     if og is not None:
         _expect(tuple(og.shape) == (B, T, H, d) and og.dtype == q.dtype, "og: [B,T,H,d] in q's dtype")
     if flags & ATTN_ROPE_Q:
@@ -548,7 +569,8 @@ def dense_attn(q, k, vt, bits, scale: float, og=None, cos=None, sin=None, flags:
     st = lib.gsa_dense_attn(_ptr(q), *_rows(q, HD), _ptr(k), *_rows(k, HD), _ptr(vt), vt.stride(0),
                             vt.stride(1), vt.shape[3], _ptr(bits), bits.stride(0), bits.stride(1),
                             _ptr(og), *os_, _ptr(cos), _ptr(sin), cs, _ptr(out), *_rows(out, HD),
-                            B, T, Tkv, H, d, float(scale), dtype_code(q.dtype), int(flags), int(bool(causal)),
+                            B, T, Tkv, H, d, float(scale), dtype_code(q.dtype),
+                            int(flags) | (ATTN_MASKS_READY if masks_ready else 0), int(bool(causal)),
                             _ptr(ws), nbytes, _stream(q))
     _check(st, "gsa_dense_attn")
     return out

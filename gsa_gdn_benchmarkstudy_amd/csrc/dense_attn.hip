@@ -586,6 +586,41 @@ extern "C" size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv) {
   return (size_t)B * groups * ((Tkv + 63) / 64) * 32 * sizeof(uint64_t);
 }
 
+namespace {
+// Checks shared by gsa_dense_lane_masks and gsa_dense_attn's mask step.
+int lane_mask_checks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv, const void* ws,
+                     size_t ws_bytes) {
+  if (!bits || !ws) return GSA_ERR_NULL;
+  if (B < 1 || T < 1 || Tkv < 1) return GSA_ERR_SHAPE;
+  const int NT = (Tkv + 63) / 64;
+  if (b_st < 2 * NT || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
+  if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
+  const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
+  const int G = nqb * (gsa::kDQ / 32);
+  if ((int64_t)B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
+  if (!aligned(bits, 8) || (b_sb % 2) || (b_st % 2) || !aligned(ws, 8)) return GSA_ERR_ALIGN;
+  return GSA_OK;
+}
+
+int launch_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv, void* ws,
+                      hipStream_t s) {
+  const int NT = (Tkv + 63) / 64;
+  const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
+  const int G = nqb * (gsa::kDQ / 32);
+  const int nwaves = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
+  hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((nwaves + 3) / 4), dim3(256), 0, s, bits, b_sb, b_st, T, G, NT,
+                     nwaves, static_cast<uint64_t*>(ws));
+  return launch_status();
+}
+}  // namespace
+
+extern "C" int gsa_dense_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv,
+                                    void* ws, size_t ws_bytes, void* stream) {
+  const int st = lane_mask_checks(bits, b_sb, b_st, B, T, Tkv, ws, ws_bytes);
+  if (st) return st;
+  return launch_lane_masks(bits, b_sb, b_st, B, T, Tkv, ws, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                               const void* k, int64_t k_sb, int64_t k_st,
                               const void* vt, int64_t vt_sb, int64_t vt_sh, int ldv,
@@ -597,15 +632,15 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                               int dtype, int flags, int causal,
                               void* ws, size_t ws_bytes,
                               void* stream) {
-  if (!q || !k || !vt || !bits || !out || !ws) return GSA_ERR_NULL;
-  if (flags & ~(GSA_ATTN_ROPE_Q | GSA_ATTN_OUT_GATE)) return GSA_ERR_FLAGS;
+  const bool ready = (flags & GSA_ATTN_MASKS_READY) != 0;
+  if (!q || !k || !vt || !out || !ws || (!ready && !bits)) return GSA_ERR_NULL;
+  if (flags & ~(GSA_ATTN_ROPE_Q | GSA_ATTN_OUT_GATE | GSA_ATTN_MASKS_READY)) return GSA_ERR_FLAGS;
   if ((flags & GSA_ATTN_ROPE_Q) && (!cos || !sin)) return GSA_ERR_NULL;
   if ((flags & GSA_ATTN_OUT_GATE) && !og) return GSA_ERR_NULL;
   if (dtype != GSA_DTYPE_BF16) return GSA_ERR_DTYPE;
   if (B < 1 || T < 1 || Tkv < 1 || d != 128 || H < 1 || H > 64) return GSA_ERR_SHAPE;
   const int NT = (Tkv + 63) / 64;
   if (ldv < NT * 64 || ldv % 64 != 0) return GSA_ERR_SHAPE;
-  if (b_st < 2 * NT || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
   if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
   // per-lane load offsets within a tile are 32-bit byte offsets
   if (k_st > (1 << 24) || (int64_t)ldv > (1 << 23)) return GSA_ERR_SHAPE;
@@ -613,18 +648,22 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   const int G = nqb * (gsa::kDQ / 32);    // 32-row groups, padded to whole blocks
   if ((int64_t)B * H * nqb > 0x7fffffffLL || (int64_t)B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
   if (!vec_ok(q, q_sb, q_st, dtype) || !vec_ok(k, k_sb, k_st, dtype) || !vec_ok(vt, vt_sb, vt_sh, dtype) ||
-      !vec_ok(out, out_sb, out_st, dtype) || !aligned(bits, 8) || (b_sb % 2) || (b_st % 2) || !aligned(ws, 8))
+      !vec_ok(out, out_sb, out_st, dtype) || !aligned(ws, 8))
     return GSA_ERR_ALIGN;
   if ((flags & GSA_ATTN_OUT_GATE) && !vec_ok(og, o_sb, o_st, dtype)) return GSA_ERR_ALIGN;
   if ((flags & GSA_ATTN_ROPE_Q) && (!vec_ok(cos, 0, cs_st, dtype) || !vec_ok(sin, 0, cs_st, dtype)))
     return GSA_ERR_ALIGN;
+  if (!ready) {
+    const int st = lane_mask_checks(bits, b_sb, b_st, B, T, Tkv, ws, ws_bytes);
+    if (st) return st;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint64_t* lm = static_cast<uint64_t*>(ws);
-  const int nwaves = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
-  hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((nwaves + 3) / 4), dim3(256), 0, s, bits, b_sb, b_st, T, G, NT,
-                     nwaves, lm);
-  int st = launch_status();
-  if (st) return st;
+  if (!ready) {
+    const int st = launch_lane_masks(bits, b_sb, b_st, B, T, Tkv, ws, s);
+    if (st) return st;
+  }
+  flags &= ~GSA_ATTN_MASKS_READY;
   gsa::DenseArgs a{static_cast<const uint16_t*>(q), q_sb, q_st, static_cast<const uint16_t*>(k), k_sb, k_st,
                    static_cast<const uint16_t*>(vt), vt_sb, vt_sh, ldv, G, NT,
                    static_cast<const uint16_t*>(og), o_sb, o_st, static_cast<const uint16_t*>(cos),

@@ -473,6 +473,12 @@ class GatedSparseAttention(nn.Module):
         return _abi.indexer_select(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale,
                                    sel.k_effective(T), indices=indices)
 
+    def _side_stream(self, dev: torch.device) -> torch.cuda.Stream:
+        """The layer's second stream (default priority), created on first use."""
+        if self._indexer_stream is None or self._indexer_stream.device != dev:
+            self._indexer_stream = torch.cuda.Stream(device=dev)
+        return self._indexer_stream
+
     def uses_dense(self, dtype: torch.dtype) -> bool:
         if self.attn_impl not in ("auto", "dense", "gather"):
             raise ValueError(f"attn_impl {self.attn_impl!r}: expected 'auto', 'dense' or 'gather'")
@@ -526,12 +532,7 @@ class GatedSparseAttention(nn.Module):
         _range_push("gsa_hip/indexer_gemm")
         views = self.project_indexer(x)
         _range_pop()
-        if mode == "serial":
-            side = cur
-        else:
-            if self._indexer_stream is None or self._indexer_stream.device != dev:
-                self._indexer_stream = torch.cuda.Stream(device=dev)
-            side = self._indexer_stream
+        side = cur if mode == "serial" else self._side_stream(dev)
         if mode == "producer":
             _range_push("gsa_hip/main_gemm")
             views.update(main_projection())
@@ -542,6 +543,19 @@ class GatedSparseAttention(nn.Module):
             _range_push("gsa_hip/indexer_select")
             bits, idx, cnt = self.select(views, T, indices=not dense)
             _range_pop()
+        # The dense attention's lane masks, built from the bitmask off the
+        # current stream (beside the projection GEMM / producer): on the
+        # indexer's side stream, or in "serial" mode on a second stream that
+        # starts after the indexer.
+        lm_ws, lm_stream = None, None
+        if dense:
+            lm_stream = side if side is not cur else self._side_stream(dev)
+            if lm_stream is not side:
+                lm_stream.wait_stream(cur)
+            with torch.cuda.stream(lm_stream):
+                _range_push("gsa_hip/lane_masks")
+                lm_ws = _abi.dense_lane_masks(bits, T)
+                _range_pop()
         if mode != "producer":
             _range_push("gsa_hip/main_gemm")
             views.update(main_projection())
@@ -563,6 +577,10 @@ class GatedSparseAttention(nn.Module):
                 if t is not None:
                     t.record_stream(cur)
             views["_ibuf"].record_stream(side)
+        if lm_stream is not None:
+            if lm_stream is not side:
+                cur.wait_stream(lm_stream)
+            lm_ws.record_stream(cur)
 
         _range_push("gsa_hip/sparse_attn")
         ev = None
@@ -572,7 +590,7 @@ class GatedSparseAttention(nn.Module):
         flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
         if dense:
             attn = _abi.dense_attn(views["q"], k_rope, v_gated, bits, self.scale, og=views["og"],
-                                   cos=cos, sin=sin, flags=flags, causal=True)
+                                   cos=cos, sin=sin, flags=flags, causal=True, ws=lm_ws, masks_ready=True)
         else:
             attn = _abi.sparse_attn(views["q"], k_rope, v_gated, idx, self.scale, count=cnt,
                                     og=views["og"], cos=cos, sin=sin, flags=flags)

@@ -52,6 +52,7 @@ extern "C" {
 /* Flags of gsa_sparse_attn */
 #define GSA_ATTN_ROPE_Q   1  /* q is pre-RoPE: apply RoPE with cos/sin in the prologue  */
 #define GSA_ATTN_OUT_GATE 2  /* multiply the output by sigmoid(og) (the G1 output gate) */
+#define GSA_ATTN_MASKS_READY 4  /* gsa_dense_attn: ws already holds gsa_dense_lane_masks of bits */
 
 /* Largest k_eff of gsa_topk_select in GSA_ORDER_SCORE_DESC order. */
 #define GSA_TOPK_DESC_MAX_K 4096
@@ -267,9 +268,21 @@ int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel
  * causal != 0: key tiles after a 256-row query block's last row are skipped
  * (the selection must then be causal).  ws: caller-provided device workspace
  * of at least gsa_dense_attn_workspace_bytes(B, T, Tkv) bytes (8-byte
- * aligned), overwritten by each call.  bf16 only; d == 128, 1 <= H <= 64.
+ * aligned), overwritten by each call -- or, with GSA_ATTN_MASKS_READY, the
+ * lane masks gsa_dense_lane_masks wrote there for the same bits, B, T and
+ * Tkv (then bits is not read).  bf16 only; d == 128, 1 <= H <= 64.
  */
 size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
+
+/*
+ * The first step of gsa_dense_attn on its own: the selection bitmask ->
+ * per-lane masks of the attention kernel's score slots, into ws (same size
+ * and alignment as gsa_dense_attn's workspace).  Lets a caller build them
+ * on another stream, beside other work, and pass GSA_ATTN_MASKS_READY.
+ * No counterpart in the reference: part of this build's dense attention.
+ */
+int gsa_dense_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st,
+                         int B, int T, int Tkv, void* ws, size_t ws_bytes, void* stream);
 
 int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                    const void* k, int64_t k_sb, int64_t k_st,

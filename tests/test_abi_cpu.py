@@ -45,7 +45,8 @@ def test_constants_match_header(lib):
     assert lib.gsa_abi_version() == m["GSA_ABI_VERSION"] == _abi.ABI_VERSION
     assert (m["GSA_DTYPE_F32"], m["GSA_DTYPE_BF16"]) == (_abi.DTYPE_F32, _abi.DTYPE_BF16)
     assert (m["GSA_ORDER_INDEX_ASC"], m["GSA_ORDER_SCORE_DESC"]) == (_abi.ORDER_INDEX_ASC, _abi.ORDER_SCORE_DESC)
-    assert (m["GSA_ATTN_ROPE_Q"], m["GSA_ATTN_OUT_GATE"]) == (_abi.ATTN_ROPE_Q, _abi.ATTN_OUT_GATE)
+    assert (m["GSA_ATTN_ROPE_Q"], m["GSA_ATTN_OUT_GATE"], m["GSA_ATTN_MASKS_READY"]) == (
+        _abi.ATTN_ROPE_Q, _abi.ATTN_OUT_GATE, _abi.ATTN_MASKS_READY)
     assert m["GSA_TOPK_DESC_MAX_K"] == _abi.TOPK_DESC_MAX_K
 
 
@@ -190,8 +191,14 @@ def test_dense_path_validation(lib):
     assert call(wsb=8 * 256 - 1) == 2             # workspace too small
     assert call(dtype=0) == 3                     # bf16 only
     assert call(ldv=32) == 2                      # rows shorter than ceil(Tkv/64)*64
-    assert call(flags=4) == 6
+    assert call(flags=8) == 6                     # unknown flag
     assert call(bst=3) == 4
+    lmk = lib.gsa_dense_lane_masks
+    assert lmk(None, 0, 2, 1, 4, 4, P, 8 * 256, None) == 1
+    assert lmk(P, 0, 2, 1, 4, 4, None, 8 * 256, None) == 1
+    assert lmk(P, 0, 2, 1, 4, 4, P, 8 * 256 - 1, None) == 2   # workspace too small
+    assert lmk(P, 0, 1, 1, 4, 4, P, 8 * 256, None) == 2       # row of W words shorter than 2*ceil(Tkv/64)
+    assert lmk(P, 0, 3, 1, 4, 4, P, 8 * 256, None) == 4       # 8-byte aligned rows
     p = lib.gsa_prologue_vt
     assert p(P, 0, 2048, P, 0, 2048, P, 0, 2048, P, P, 128, 1, 4, 16, 128, 1, P, P, 100, None) == 2   # ldv % 64
     assert p(P, 0, 2048, None, 0, 2048, P, 0, 2048, P, P, 128, 1, 4, 16, 128, 1, P, P, 64, None) == 1

@@ -392,3 +392,27 @@ def test_dense_attention_noncausal_selection(dev):
     mask = torch.arange(k)[None, None, :] < cnt[..., None]
     ref = orc.sparse_attention(q.double(), kk.double(), v.double(), ia, mask, 0.1)
     assert (torch.linalg.vector_norm(out.double() - ref) / torch.linalg.vector_norm(ref)).item() < 5e-3
+
+
+def test_dense_lane_masks_then_attention_equals_one_call(dev):
+    """gsa_dense_lane_masks on another stream, then gsa_dense_attn with
+    GSA_ATTN_MASKS_READY: the same output as the one-call path, bit for bit."""
+    B, T, H, k = 2, 300, 4, 64
+    q, kk, v, og, ia, cnt = _dense_case(B, T, H, k, seed=91)
+    cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
+    qd, kd, ogd = q.to(dev), kk.to(dev), og.to(dev)
+    cosd, sind = cos.to(dev), sin.to(dev)
+    vt = torch.zeros(B, H, 128, _abi.vt_len(T), dtype=torch.bfloat16, device=dev)
+    vt[..., :T] = v.to(dev).permute(0, 2, 3, 1)
+    bits = _abi.selection_mask(ia.to(dev), T, count=cnt.to(dev))
+    flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
+    one = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, og=ogd, cos=cosd, sin=sind, flags=flags)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        ws = _abi.dense_lane_masks(bits, T)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    two = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, og=ogd, cos=cosd, sin=sind, flags=flags,
+                          ws=ws, masks_ready=True)
+    torch.cuda.synchronize()
+    assert torch.equal(one.cpu(), two.cpu())
