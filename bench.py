@@ -290,7 +290,10 @@ def main():
     gather_roof = {"kernel": "gsa_sparse_attn", "bound": "hbm", "achieved": gather_gbs, "peak": HBM_PEAK_GBS,
                    "unit": "GB/s", "frac": gather_gbs / HBM_PEAK_GBS,
                    "traffic": profiled_traffic("gsa_sparse_attn", args.config),
-                   "algorithmic_bytes": abytes, "valid_pairs": P, "ms": gather_ms}
+                   "algorithmic_bytes": abytes, "valid_pairs": P, "ms": gather_ms,
+                   "note": "algorithmic bytes count every selected K/V row as an HBM read; rows that "
+                           "many queries select are served from L2 and the last-level cache, so the "
+                           "rate can exceed the HBM peak"}
     if attn_impl == "dense":
         qrows = 256                              # query rows per block of gsa_dense_attn
         nqb = (T + qrows - 1) // qrows
