@@ -289,18 +289,21 @@ class OutputGate(nn.Module):
 class GatedSparseAttention(nn.Module):
     """Drop-in replacement for gsa_ref/gsa_opt.GatedSparseAttention.
 
-    Forward, per layer call:
+    Forward, per layer call (two streams; ``indexer_overlap`` places step 2):
       1. the indexer projections (one small GEMM over the fused weight's last,
-         zero-padded 64-aligned row block), then the q/k/v/gate GEMM; the slices
-         are strided views, never copied;
-      2. indexer stream (concurrent with the q/k/v/gate GEMM):
-         gsa_indexer_select -- MFMA indexer fused with the
-         exact top-k, writing ascending int32 indices and per-row counts
-         (the T x T score matrix is never stored) -- and, for the dense
-         attention, gsa_selection_mask (the selection as a bitmask);
-         current stream: RoPE(k) and v * sigmoid(vg) (gsa_prologue_vt, V
+         zero-padded 64-aligned row block) and the q/k/v/gate GEMM; the slices
+         are strided views, never copied (``proj_impl="fused"``: one MFMA GEMM
+         with step 3's producer in its epilogue instead);
+      2. gsa_indexer_select -- MFMA indexer fused with the exact top-k,
+         writing the selection as a bitmask, and for the gather attention
+         ascending int32 indices with per-row counts (the T x T score matrix
+         is never stored) -- beside the q/k/v/gate GEMM while its grid leaves
+         CUs free, before it while RoPE(k) and V^T fit the last-level cache,
+         else beside the producer; the dense attention's lane masks
+         (gsa_dense_lane_masks) follow on the second stream;
+      3. current stream: RoPE(k) and v * sigmoid(vg) (gsa_prologue_vt, V
          transposed, or gsa_prologue);
-      3. join, then the attention with RoPE(q) and the output gate fused --
+      4. join, then the attention with RoPE(q) and the output gate fused --
          gsa_dense_attn (bf16: MFMA over every causal key tile, masked to the
          selection) or gsa_sparse_attn (per-row gather of the selected keys)
          -- and the o_proj GEMM.
