@@ -150,7 +150,7 @@ def test_layer_vs_oracle_small(dev, dtype, impl, B, T):
 
 
 def test_layer_c1_fp32(dev):
-    """configs[0] shape: D=2048, H=16, T=512, k_base=256, k_max=512, fp32."""
+    """The CPU-runnable reference workload: D=2048, H=16, T=512, k_base=256, k_max=512, fp32."""
     _log("layer c1 fp32 T=512")
     cfg = orc.GSAConfig(hidden_size=2048, num_heads=16, k_max=512, k_base=256, k_min=64)
     sd = orc.synthetic_state(cfg, seed=0)
@@ -170,7 +170,7 @@ def test_layer_c1_fp32(dev):
 
 @pytest.mark.parametrize("impl", ["dense", "gather"])
 def test_layer_c2_bf16_sampled_rows(dev, impl):
-    """configs[1] shape: T=4096, D=2048, bf16, k=2048 -- oracle on sampled row blocks."""
+    """T=4096, D=2048, bf16, k=2048 -- oracle on sampled row blocks."""
     _log(f"layer c2 bf16 T=4096 (sampled rows) impl={impl}")
     cfg = orc.GSAConfig(hidden_size=2048, num_heads=16, k_max=4096, k_base=2048, k_min=256)
     sd = orc.cast_state(orc.synthetic_state(cfg, seed=0), torch.bfloat16)
