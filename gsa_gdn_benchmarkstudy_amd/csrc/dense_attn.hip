@@ -1,5 +1,5 @@
 // Block-dense sparse attention on gfx950 MFMA: every causal key tile is
-// streamed once per 128-row query block and the exact top-k selection is
+// streamed once per 256-row query block and the exact top-k selection is
 // applied as a bitmask, so masked-out keys get probability 0.  Same function
 // as the gather kernel (softmax over each row's selected keys), different
 // work: dense MFMA over the causal triangle instead of per-row gathers.
@@ -9,7 +9,7 @@
 // selection bits [B,T,W] uint32, W = 2*ceil(Tkv/64): bit j of row t set iff
 // key j is selected and valid for query t.
 //
-// Per block: one head, 128 query rows, 4 waves of 32 rows, 64-key tiles
+// Per block: one head, 256 query rows, 8 waves of 32 rows, 64-key tiles
 // in LDS.  With v_mfma_f32_32x32x16_bf16 both products are computed
 // transposed,
 //   S^T = K Q^T    (A = K tile from LDS, B = this wave's q, in registers)
@@ -165,10 +165,11 @@ __global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restri
 // ---------------------------------------------------------------------------
 // Dense masked attention (bf16)
 //
-// Block: 4 waves = 128 query rows of one head (wave w: rows 32w .. 32w+31).
-// K and V^T tiles reach LDS by direct global->LDS loads (16 B per lane; one
-// instruction fills 1 KiB, lane-linear), double-buffered, in padded layouts
-// (unit = 16 B = 8 bf16):
+// Block: kDW = 8 waves = 256 query rows of one head (wave w: rows 32w ..
+// 32w+31), two waves per SIMD.  K and V^T tiles reach LDS by direct
+// global->LDS loads (16 B per lane; one instruction fills 1 KiB,
+// lane-linear), K tiles and V^T tiles each through a pair of slots, in padded
+// layouts (unit = 16 B = 8 bf16):
 //   K   tile: 64 keys x 17 units, unit 16 of a key is padding
 //   V^T tile: 128 rows x 9 units (64 keys), unit 8 of a row is padding
 // The odd row strides make every MFMA operand read conflict-free (16 lanes
@@ -180,10 +181,10 @@ __global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restri
 // holds key 16(r/8) + 8h + r%8.  A lane's 8 P values of each 16-key k-step
 // are then contiguous keys, and its V^T operand is one 16-byte read.
 //
-// Per tile the two halves are pipelined: S^T of half 1 is computed while the
-// softmax of half 0 runs, and O^T += V^T P^T of half 0 while the softmax of
-// half 1 runs, so MFMA and VALU work of one wave overlap.  Each half is one
-// online-softmax step with the lazy reference (below).
+// Tiles are pipelined: S^T of tile t+1 (both 32-key halves) is computed
+// while the softmax of tile t runs, then O^T += V^T(t) P^T(t), so MFMA and
+// VALU work of one wave overlap.  Each 64-key tile is one online-softmax step
+// with the lazy reference (below).
 // ---------------------------------------------------------------------------
 struct DenseArgs {
   const uint16_t* q; int64_t q_sb, q_st;
@@ -586,7 +587,7 @@ extern "C" int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st
 }
 
 // Lane masks: 32 per (batch, 32-row group, 64-key tile); the groups are
-// counted over whole 128-row query blocks.
+// counted over whole 256-row query blocks.
 extern "C" size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv) {
   if (B < 1 || T < 1 || Tkv < 1) return 0;
   const size_t groups = (size_t)((T + gsa::kDQ - 1) / gsa::kDQ) * (gsa::kDQ / 32);
