@@ -223,12 +223,6 @@ __device__ __forceinline__ float sum_halves(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Two fp32 -> packed bf16 (round to nearest even, hardware convert).
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
-  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
 // 32-bit LDS address of a shared-memory pointer.
 __device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
@@ -429,7 +423,7 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
       for (int r = 0; r < 16; r += 2) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[c][r], p.scale_l2, -msafe));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[c][r + 1], p.scale_l2, -msafe));
-        pk[2 * c + (r >> 3)][(r & 7) >> 1] = cvt_pk_bf16(p0, p1);
+        pk[2 * c + (r >> 3)][(r & 7) >> 1] = pack_bf16(p0, p1);
         lsum += p0 + p1;
       }
     l = l * alpha + lsum;

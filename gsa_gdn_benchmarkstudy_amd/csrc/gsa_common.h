@@ -22,22 +22,22 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
 // bf16 <-> fp32.  Rounding is round-to-nearest-even, the rounding torch uses
-// when an fp32 intermediate is stored as bf16; NaN stays a quiet NaN.
+// when an fp32 intermediate is stored as bf16, done by the hardware convert
+// (v_cvt_pk_bf16_f32; two values per instruction in pack_bf16); NaN stays
+// NaN.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf16lo(uint32_t packed) { return __uint_as_float(packed << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ float round_bf16(float f) {
   return __uint_as_float(f32_to_bf16_bits(f) << 16);
 }
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // Storage-type traits: how one 16-lane head slice of 8 elements is held.
