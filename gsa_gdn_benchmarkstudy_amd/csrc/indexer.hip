@@ -577,16 +577,26 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_bits_kernel(IdxArgs p, 
       if (lane == 0) { st_mode[rl] = kOverflow; st_any[1] = 1; }
       continue;
     }
+    // The row's n candidates, compacted: candidate j (in the regions' order)
+    // goes to slot j / 64, lane j % 64, so the radix passes below ballot
+    // ceil(n / 64) slots instead of one per occupied region half.
     constexpr int kSlots = kCap / 64;
+    int start[kGroupWaves];
+    int n = 0;
+#pragma unroll
+    for (int w = 0; w < kGroupWaves; ++w) { start[w] = n; n += nw[w]; }
     uint32_t cv[kSlots], ci[kSlots];
     bool cvalid[kSlots], used[kSlots];
     uint32_t kor = 0u, kand = ~0u;
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
-      const int w = i >> 1, pos = (i & 1) * 64 + lane;
-      used[i] = (i & 1) * 64 < nw[w];
-      cvalid[i] = pos < nw[w];
-      const uint2 cd = cvalid[i] ? cand[rl * kCap + w * kWCap + pos] : uint2{0u, 0u};
+      const int j = i * 64 + lane;
+      used[i] = i * 64 < n;
+      cvalid[i] = j < n;
+      int w = 0;
+#pragma unroll
+      for (int ww = 1; ww < kGroupWaves; ++ww) w += j >= start[ww] ? 1 : 0;
+      const uint2 cd = cvalid[i] ? cand[rl * kCap + w * kWCap + (j - start[w])] : uint2{0u, 0u};
       cv[i] = cd.x;
       ci[i] = cd.y;
       if (cvalid[i]) { kor |= cv[i]; kand &= cv[i]; }
