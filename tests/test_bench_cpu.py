@@ -1,0 +1,39 @@
+"""bench.py's contract pieces that run without a GPU: more than one GPU is refused
+with a message, and the HBM traffic of the roofline objects comes from the committed
+rocprofv3 summaries (one `traffic_bytes <kernel> <config> <bytes>` line each)."""
+
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.mark.parametrize("n", [2, 8])
+def test_bench_refuses_more_than_one_gpu(n):
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", str(n)],
+                       capture_output=True, text=True, timeout=300, cwd=ROOT)
+    assert r.returncode == 2
+    assert "measures one GPU" in r.stderr and f"--gpus {n}" in r.stderr
+    assert r.stdout == ""             # no JSON line
+
+
+def test_profiled_traffic_lines():
+    sys.path.insert(0, ROOT)
+    try:
+        import bench
+    finally:
+        sys.path.remove(ROOT)
+    dense = bench.profiled_traffic("gsa_dense_attn", "c3")
+    idx = bench.profiled_traffic("gsa_indexer_select", "c3")
+    gather = bench.profiled_traffic("gsa_sparse_attn", "c3")
+    # each kernel's HBM bytes per launch at c3, from FETCH_SIZE/WRITE_SIZE: the dense
+    # kernel streams K and V^T tiles (128 MiB) through L2 many times, the indexer
+    # writes and reads back its 537 MB of score tiles, the gather kernel misses L2
+    # on most of its 258 GB of gathered rows
+    assert dense is not None and 0.5e9 < dense < 5e9
+    assert idx is not None and 1.07e9 < idx < 2e9
+    assert gather is not None and 1e11 < gather < 3e11
+    assert bench.profiled_traffic("gsa_dense_attn", "c9") is None
