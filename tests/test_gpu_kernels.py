@@ -209,12 +209,17 @@ def test_indexer_select_long_rows_T65536(dev):
     assert same / total >= 0.999
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
-def test_prologue_vs_oracle(dev, dtype):
+@pytest.mark.parametrize("dtype,k_scale", [(torch.bfloat16, 1.0), (torch.float32, 1.0),
+                                           (torch.bfloat16, 1e-37), (torch.bfloat16, 1e37)])
+def test_prologue_vs_oracle(dev, dtype, k_scale):
+    """RoPE(k) bit-exact with the oracle's bf16 ops (every product and sum rounded to
+    bf16, round-to-nearest-even; random bf16 operands hit exact ties about once per
+    256 products); k_scale 1e-37 puts the products and sums among fp32 subnormals,
+    1e37 near the top of the range."""
     B, T, H = 2, 40, 4
-    _log(f"prologue dtype={dtype}")
+    _log(f"prologue dtype={dtype} k_scale={k_scale}")
     g = torch.Generator().manual_seed(1)
-    k = torch.randn(B, T, H, 128, generator=g).to(dtype)
+    k = (torch.randn(B, T, H, 128, generator=g) * k_scale).to(dtype)
     v = torch.randn(B, T, H, 128, generator=g).to(dtype)
     vg = (torch.randn(B, T, H, 128, generator=g) * 3).to(dtype)
     cos, sin = orc.RopeCache(128, dtype).tables(T, dtype)
