@@ -38,6 +38,7 @@ EXPORTS = (
     "gsa_indexer_select_workspace_bytes", "gsa_indexer_select_adaptive",
     "gsa_indexer_select_adaptive_workspace_bytes", "gsa_topk_select_adaptive",
     "gsa_proj_packed_bytes", "gsa_proj_pack", "gsa_proj_fused", "gsa_dense_lane_masks",
+    "gsa_prologue_vt_lane_masks",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -73,6 +74,9 @@ _PROTOS = {
     "gsa_dense_attn_workspace_bytes": ([_i32, _i32, _i32], ctypes.c_size_t),
     "gsa_proj_packed_bytes": ([_i32, _i32], ctypes.c_size_t),
     "gsa_dense_lane_masks": ([_vp, _i64, _i64, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
+    "gsa_prologue_vt_lane_masks": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
+                                    _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32,
+                                    _vp, _i64, _i64, _i32, _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_proj_pack": ([_vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
     "gsa_proj_fused": ([_vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64,
                         _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], _i32),
@@ -403,10 +407,14 @@ def mask_words(Tkv: int) -> int:
     return 2 * ((Tkv + 63) // 64)
 
 
-def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None):
-    """RoPE(k) -> k_out [B,T,H,d] and (v*sigmoid(vg))^T -> vt [B,H,d,ldv] (bf16)."""
+def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None, bits=None, Tkv=None, ws=None):
+    """RoPE(k) -> k_out [B,T,H,d] and (v*sigmoid(vg))^T -> vt [B,H,d,ldv] (bf16).
+
+    With ``bits`` (the selection bitmask [B,T,W] of keys 0..Tkv-1): the dense
+    attention's lane masks are built in the same launch (gsa_prologue_vt_lane_masks)
+    into ``ws`` (allocated when None), returned third: (k_out, vt, ws)."""
     lib = load()
-    _need_cuda(k, v, vg, cos, sin)
+    _need_cuda(k, v, vg, cos, sin, bits, ws)
     B, T, H, d = v.shape
     HD = H * d
     ldv = vt_len(T)
@@ -426,11 +434,25 @@ def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None):
             "vt: contiguous [B,H,d,ldv]")
     ks = _rows(k, HD) if k is not None else (0, 0)
     cs = cos.stride(0) if cos is not None else 0
-    st = lib.gsa_prologue_vt(_ptr(k), *ks, _ptr(v), *_rows(v, HD), _ptr(vg), *_rows(vg, HD), _ptr(cos),
-                             _ptr(sin), cs, B, T, H, d, dtype_code(v.dtype), _ptr(k_out), _ptr(vt), ldv,
-                             _stream(v))
-    _check(st, "gsa_prologue_vt")
-    return k_out, vt
+    if bits is None:
+        st = lib.gsa_prologue_vt(_ptr(k), *ks, _ptr(v), *_rows(v, HD), _ptr(vg), *_rows(vg, HD), _ptr(cos),
+                                 _ptr(sin), cs, B, T, H, d, dtype_code(v.dtype), _ptr(k_out), _ptr(vt), ldv,
+                                 _stream(v))
+        _check(st, "gsa_prologue_vt")
+        return k_out, vt
+    Tkv = T if Tkv is None else Tkv
+    _expect(tuple(bits.shape) == (B, T, mask_words(Tkv)) and bits.stride(2) == 1 and bits.dtype == torch.int32,
+            "bits: int32 [B,T,W]")
+    nbytes = lib.gsa_dense_attn_workspace_bytes(B, T, Tkv)
+    if ws is None:
+        ws = torch.empty(nbytes, device=v.device, dtype=torch.uint8)
+    _expect(ws.numel() * ws.element_size() >= nbytes and ws.is_contiguous(), "workspace too small")
+    st = lib.gsa_prologue_vt_lane_masks(_ptr(k), *ks, _ptr(v), *_rows(v, HD), _ptr(vg), *_rows(vg, HD), _ptr(cos),
+                                        _ptr(sin), cs, B, T, H, d, dtype_code(v.dtype), _ptr(k_out), _ptr(vt),
+                                        ldv, _ptr(bits), bits.stride(0), bits.stride(1), Tkv, _ptr(ws), nbytes,
+                                        _stream(v))
+    _check(st, "gsa_prologue_vt_lane_masks")
+    return k_out, vt, ws
 
 
 def proj_supported(D: int, H: int, T: int) -> bool:

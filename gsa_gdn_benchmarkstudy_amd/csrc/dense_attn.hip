@@ -43,10 +43,10 @@ struct ProVtArgs {
   int T, H, ldv, ntiles;
 };
 
-__global__ __launch_bounds__(256) void prologue_vt_kernel(ProVtArgs p) {
-  __shared__ __align__(16) uint16_t sV[kDK * kKS];
-  const int kt = blockIdx.x % p.ntiles;
-  const int bh = blockIdx.x / p.ntiles;
+// Block `blk` of the producer (one (b, h, 64-key tile)); sV: kDK * kKS elements of LDS.
+__device__ __forceinline__ void prologue_vt_block(const ProVtArgs& p, int blk, uint16_t* sV) {
+  const int kt = blk % p.ntiles;
+  const int bh = blk / p.ntiles;
   const int h = bh % p.H, b = bh / p.H;
   const int j0 = kt * kDK;
   const int tid = threadIdx.x, li = tid & 15;
@@ -91,6 +91,11 @@ __global__ __launch_bounds__(256) void prologue_vt_kernel(ProVtArgs p) {
   }
 }
 
+__global__ __launch_bounds__(256) void prologue_vt_kernel(ProVtArgs p) {
+  __shared__ __align__(16) uint16_t sV[kDK * kKS];
+  prologue_vt_block(p, blockIdx.x, sV);
+}
+
 // ---------------------------------------------------------------------------
 // Selection bitmask from (indices, count, mask): one block per row.
 // ---------------------------------------------------------------------------
@@ -129,11 +134,20 @@ __global__ __launch_bounds__(256) void selection_mask_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kLmTiles = 4;
 
-__global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restrict__ bits, int64_t b_sb,
-                                                        int64_t b_st, int T, int G, int NT, int nwaves,
-                                                        uint64_t* __restrict__ lm) {
-  const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wv >= nwaves) return;
+struct LaneMaskArgs {
+  const uint32_t* bits; int64_t b_sb, b_st;
+  int T, G, NT, nwaves;
+  uint64_t* lm;
+};
+
+// Block `blk` of the lane-mask pass: its 4 waves take waves 4*blk .. 4*blk+3.
+__device__ __forceinline__ void lane_mask_block(const LaneMaskArgs& a, int blk) {
+  const uint32_t* __restrict__ bits = a.bits;
+  uint64_t* __restrict__ lm = a.lm;
+  const int64_t b_sb = a.b_sb, b_st = a.b_st;
+  const int T = a.T, G = a.G, NT = a.NT;
+  const int wv = blk * 4 + (threadIdx.x >> 6);
+  if (wv >= a.nwaves) return;
   const int nq = (NT + kLmTiles - 1) / kLmTiles;
   const int kq = wv % nq, bg = wv / nq;
   const int g = bg % G, b = bg / G;
@@ -160,6 +174,22 @@ __global__ __launch_bounds__(256) void lane_mask_kernel(const uint32_t* __restri
       }
     if (lane < 32) lm[((int64_t)bg * NT + kt0 + u) * 32 + lane] = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
   }
+}
+
+__global__ __launch_bounds__(256) void lane_mask_kernel(LaneMaskArgs a) { lane_mask_block(a, blockIdx.x); }
+
+// The producer and the lane-mask pass in one launch, their blocks interleaved
+// evenly over the grid so that both kinds run side by side: block b is a
+// lane-mask block iff c(b+1) > c(b), c(b) = floor(b * n_lm / (n_pro + n_lm))
+// (the number of lane-mask blocks before b), with lane-mask index c(b) and
+// producer index b - c(b).
+__global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p, LaneMaskArgs l, int n_pro,
+                                                                    int n_lm) {
+  __shared__ __align__(16) uint16_t sV[kDK * kKS];
+  const int64_t total = (int64_t)n_pro + n_lm, b = blockIdx.x;
+  const int c0 = (int)(b * n_lm / total), c1 = (int)((b + 1) * n_lm / total);
+  if (c1 > c0) lane_mask_block(l, c0);
+  else prologue_vt_block(p, (int)(b - c0), sV);
 }
 
 // ---------------------------------------------------------------------------
@@ -537,13 +567,10 @@ using namespace gsa_host;
 static constexpr int kMaxDevices = 64;
 static bool g_dense_lds_set[kMaxDevices] = {};
 
-extern "C" int gsa_prologue_vt(const void* k, int64_t k_sb, int64_t k_st,
-                               const void* v, int64_t v_sb, int64_t v_st,
-                               const void* vg, int64_t g_sb, int64_t g_st,
-                               const void* cos, const void* sin, int64_t cs_st,
-                               int B, int T, int H, int d, int dtype,
-                               void* k_out, void* vt, int ldv,
-                               void* stream) {
+namespace {
+int prologue_vt_checks(const void* k, int64_t k_sb, int64_t k_st, const void* v, int64_t v_sb, int64_t v_st,
+                       const void* vg, int64_t g_sb, int64_t g_st, const void* cos, const void* sin,
+                       int64_t cs_st, int B, int T, int H, int d, int dtype, void* k_out, void* vt, int ldv) {
   if (!v || !vg || !vt) return GSA_ERR_NULL;
   if (k && (!cos || !sin || !k_out)) return GSA_ERR_NULL;
   if (dtype != GSA_DTYPE_BF16) return GSA_ERR_DTYPE;
@@ -554,6 +581,20 @@ extern "C" int gsa_prologue_vt(const void* k, int64_t k_sb, int64_t k_st,
   if (k && (!vec_ok(k, k_sb, k_st, dtype) || !vec_ok(cos, 0, cs_st, dtype) || !vec_ok(sin, 0, cs_st, dtype) ||
             !aligned(k_out, 16)))
     return GSA_ERR_ALIGN;
+  return GSA_OK;
+}
+}  // namespace
+
+extern "C" int gsa_prologue_vt(const void* k, int64_t k_sb, int64_t k_st,
+                               const void* v, int64_t v_sb, int64_t v_st,
+                               const void* vg, int64_t g_sb, int64_t g_st,
+                               const void* cos, const void* sin, int64_t cs_st,
+                               int B, int T, int H, int d, int dtype,
+                               void* k_out, void* vt, int ldv,
+                               void* stream) {
+  const int st = prologue_vt_checks(k, k_sb, k_st, v, v_sb, v_st, vg, g_sb, g_st, cos, sin, cs_st, B, T, H, d,
+                                    dtype, k_out, vt, ldv);
+  if (st) return st;
   gsa::ProVtArgs a{static_cast<const uint16_t*>(k), k_sb, k_st, static_cast<const uint16_t*>(v), v_sb, v_st,
                    static_cast<const uint16_t*>(vg), g_sb, g_st, static_cast<const uint16_t*>(cos),
                    static_cast<const uint16_t*>(sin), cs_st, static_cast<uint16_t*>(k_out),
@@ -604,14 +645,19 @@ int lane_mask_checks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, in
   return GSA_OK;
 }
 
-int launch_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv, void* ws,
-                      hipStream_t s) {
+gsa::LaneMaskArgs lane_mask_args(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv,
+                                  void* ws) {
   const int NT = (Tkv + 63) / 64;
   const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
   const int G = nqb * (gsa::kDQ / 32);
   const int nwaves = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
-  hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((nwaves + 3) / 4), dim3(256), 0, s, bits, b_sb, b_st, T, G, NT,
-                     nwaves, static_cast<uint64_t*>(ws));
+  return gsa::LaneMaskArgs{bits, b_sb, b_st, T, G, NT, nwaves, static_cast<uint64_t*>(ws)};
+}
+
+int launch_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv, void* ws,
+                      hipStream_t s) {
+  const gsa::LaneMaskArgs l = lane_mask_args(bits, b_sb, b_st, B, T, Tkv, ws);
+  hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((l.nwaves + 3) / 4), dim3(256), 0, s, l);
   return launch_status();
 }
 }  // namespace
@@ -621,6 +667,30 @@ extern "C" int gsa_dense_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t 
   const int st = lane_mask_checks(bits, b_sb, b_st, B, T, Tkv, ws, ws_bytes);
   if (st) return st;
   return launch_lane_masks(bits, b_sb, b_st, B, T, Tkv, ws, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gsa_prologue_vt_lane_masks(const void* k, int64_t k_sb, int64_t k_st,
+                                          const void* v, int64_t v_sb, int64_t v_st,
+                                          const void* vg, int64_t g_sb, int64_t g_st,
+                                          const void* cos, const void* sin, int64_t cs_st,
+                                          int B, int T, int H, int d, int dtype,
+                                          void* k_out, void* vt, int ldv,
+                                          const uint32_t* bits, int64_t b_sb, int64_t b_st, int Tkv,
+                                          void* ws, size_t ws_bytes, void* stream) {
+  int st = prologue_vt_checks(k, k_sb, k_st, v, v_sb, v_st, vg, g_sb, g_st, cos, sin, cs_st, B, T, H, d, dtype,
+                              k_out, vt, ldv);
+  if (st) return st;
+  if ((st = lane_mask_checks(bits, b_sb, b_st, B, T, Tkv, ws, ws_bytes))) return st;
+  gsa::ProVtArgs a{static_cast<const uint16_t*>(k), k_sb, k_st, static_cast<const uint16_t*>(v), v_sb, v_st,
+                   static_cast<const uint16_t*>(vg), g_sb, g_st, static_cast<const uint16_t*>(cos),
+                   static_cast<const uint16_t*>(sin), cs_st, static_cast<uint16_t*>(k_out),
+                   static_cast<uint16_t*>(vt), T, H, ldv, ldv / 64};
+  const gsa::LaneMaskArgs l = lane_mask_args(bits, b_sb, b_st, B, T, Tkv, ws);
+  const int n_pro = B * H * (ldv / 64), n_lm = (l.nwaves + 3) / 4;
+  if ((int64_t)n_pro + n_lm > 0x7fffffffLL) return GSA_ERR_SHAPE;
+  hipLaunchKernelGGL(gsa::prologue_vt_lane_mask_kernel, dim3(n_pro + n_lm), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a, l, n_pro, n_lm);
+  return launch_status();
 }
 
 extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,

@@ -300,7 +300,8 @@ class GatedSparseAttention(nn.Module):
          is never stored) -- beside the q/k/v/gate GEMM while its grid leaves
          CUs free, before it while RoPE(k) and V^T fit the last-level cache,
          else beside the producer; the dense attention's lane masks
-         (gsa_dense_lane_masks) follow on the second stream;
+         (gsa_dense_lane_masks) follow on the second stream (with the
+         indexer on the current stream: built in the producer's launch);
       3. current stream: RoPE(k) and v * sigmoid(vg) (gsa_prologue_vt, V
          transposed, or gsa_prologue);
       4. join, then the attention with RoPE(q) and the output gate fused --
@@ -358,6 +359,11 @@ class GatedSparseAttention(nn.Module):
         # with that producer in its epilogue; needs an even head count and
         # T % 64 == 0, else "gemm" runs).
         self.proj_impl = "gemm"
+        # When the indexer runs on the current stream ("serial" placement), the
+        # dense attention's lane masks are built by the producer's launch
+        # (gsa_prologue_vt_lane_masks) instead of on a second stream beside
+        # the GEMM: no join before the attention, and the GEMM has the GPU.
+        self.lane_masks_with_producer = True
         # Optional per-kernel timing hook: a list to which forward appends
         # (start, end) event pairs around the sparse-attention launch.
         self.attn_events: Optional[list] = None
@@ -547,11 +553,13 @@ class GatedSparseAttention(nn.Module):
             bits, idx, cnt = self.select(views, T, indices=not dense)
             _range_pop()
         # The dense attention's lane masks, built from the bitmask off the
-        # current stream (beside the projection GEMM / producer): on the
-        # indexer's side stream, or in "serial" mode on a second stream that
-        # starts after the indexer.
+        # current stream (beside the projection GEMM / producer) on the
+        # indexer's side stream; in "serial" mode by the producer's own launch
+        # (lane_masks_with_producer), else on a second stream that starts after
+        # the indexer.
         lm_ws, lm_stream = None, None
-        if dense:
+        lm_in_producer = (dense and not fused_proj and mode == "serial" and self.lane_masks_with_producer)
+        if dense and not lm_in_producer:
             lm_stream = side if side is not cur else self._side_stream(dev)
             if lm_stream is not side:
                 lm_stream.wait_stream(cur)
@@ -568,6 +576,9 @@ class GatedSparseAttention(nn.Module):
         _range_push("gsa_hip/prologue")
         if fused_proj:
             k_rope, v_gated = views["_k_rope"], views["_vt"]
+        elif lm_in_producer:
+            k_rope, v_gated, lm_ws = _abi.prologue_vt(views["v"], views["vg"], k=views["k"], cos=cos, sin=sin,
+                                                      bits=bits, Tkv=T)
         elif dense:
             k_rope, v_gated = _abi.prologue_vt(views["v"], views["vg"], k=views["k"], cos=cos, sin=sin)
         else:

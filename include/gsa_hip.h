@@ -284,6 +284,22 @@ size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
 int gsa_dense_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st,
                          int B, int T, int Tkv, void* ws, size_t ws_bytes, void* stream);
 
+/*
+ * gsa_prologue_vt (RoPE(k) and v*sigmoid(vg) as V^T: gsa_opt.py:685-697) and
+ * gsa_dense_lane_masks in one launch, their blocks interleaved so that both
+ * run side by side; same arguments, checks and outputs as the two calls.
+ * For callers that build the lane masks on the producer's stream right
+ * before gsa_dense_attn (no second stream, no join).
+ */
+int gsa_prologue_vt_lane_masks(const void* k, int64_t k_sb, int64_t k_st,
+                               const void* v, int64_t v_sb, int64_t v_st,
+                               const void* vg, int64_t g_sb, int64_t g_st,
+                               const void* cos, const void* sin, int64_t cs_st,
+                               int B, int T, int H, int d, int dtype,
+                               void* k_out, void* vt, int ldv,
+                               const uint32_t* bits, int64_t b_sb, int64_t b_st, int Tkv,
+                               void* ws, size_t ws_bytes, void* stream);
+
 int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                    const void* k, int64_t k_sb, int64_t k_st,
                    const void* vt, int64_t vt_sb, int64_t vt_sh, int ldv,

@@ -421,3 +421,26 @@ def test_dense_lane_masks_then_attention_equals_one_call(dev):
                           ws=ws, masks_ready=True)
     torch.cuda.synchronize()
     assert torch.equal(one.cpu(), two.cpu())
+
+
+@pytest.mark.parametrize("B,T,H", [(1, 100, 2), (2, 256, 4), (1, 700, 3)])
+def test_prologue_vt_lane_masks_equals_two_launches(dev, B, T, H):
+    """gsa_prologue_vt_lane_masks (producer and lane masks in one launch, blocks
+    interleaved) writes exactly what gsa_prologue_vt and gsa_dense_lane_masks write."""
+    _log(f"prologue_vt+lane masks B={B} T={T} H={H}")
+    g = torch.Generator().manual_seed(T + H)
+    k = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16).to(dev)
+    vg = (torch.randn(B, T, H, 128, generator=g) * 3).to(torch.bfloat16).to(dev)
+    cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
+    cos, sin = cos.to(dev), sin.to(dev)
+    s = torch.rand(B, T, T, generator=g).masked_fill(torch.triu(torch.ones(T, T, dtype=torch.bool), 1), float("-inf"))
+    idx, mask = orc.select_topk(s, min(40, T))
+    bits = _abi.selection_mask(idx.to(torch.int32).to(dev), T, mask=mask.to(dev))
+    ko, vt = _abi.prologue_vt(v, vg, k=k, cos=cos, sin=sin)
+    lm = _abi.dense_lane_masks(bits, T)
+    ko2, vt2, lm2 = _abi.prologue_vt(v, vg, k=k, cos=cos, sin=sin, bits=bits, Tkv=T)
+    torch.cuda.synchronize()
+    assert torch.equal(ko.cpu(), ko2.cpu()) and torch.equal(vt.cpu(), vt2.cpu())
+    # the masks cover every (group, causal tile) the attention reads; both calls write the same words
+    assert torch.equal(lm.cpu(), lm2.cpu())

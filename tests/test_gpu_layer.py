@@ -213,7 +213,8 @@ def test_layer_repeat_is_deterministic(dev):
 
 def test_indexer_overlap_modes_identical(dev):
     """Every stream arrangement of the indexer (beside the GEMM, beside the
-    producer, serial, auto) computes the same output bit for bit."""
+    producer, serial with the lane masks in the producer's launch or on a second
+    stream, auto) computes the same output bit for bit."""
     cfg = orc.GSAConfig(hidden_size=512, num_heads=4, k_max=96, k_base=64, k_min=16)
     sd = orc.cast_state(orc.synthetic_state(cfg, seed=5), torch.bfloat16)
     x = orc.synthetic_input(2, 300, cfg.hidden_size, seed=6).to(torch.bfloat16).to(dev)
@@ -223,6 +224,11 @@ def test_indexer_overlap_modes_identical(dev):
         for mode in ("gemm", "producer", "serial", "auto"):
             m.indexer_overlap = mode
             outs.append(m(x))
+        # serial placement with the lane masks on a second stream instead of in
+        # the producer's launch
+        m.indexer_overlap, m.lane_masks_with_producer = "serial", False
+        outs.append(m(x))
+        m.lane_masks_with_producer = True
         m.indexer_overlap = "sideways"
         with pytest.raises(ValueError):
             m(x)
