@@ -722,12 +722,17 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_bits_kernel(IdxArgs p, 
 }
 
 // ---------------------------------------------------------------------------
-// Bitmask -> ascending indices + count, one 256-thread block per row.  The
-// tail of a row with fewer than k selected keys is t+1, t+2, ... (the
-// lowest-index invalid entries, as the selector orders them).
+// Bitmask -> ascending indices + count, one 256-thread block per row.  Row
+// t of width k_eff holds its n = min(t+1, k_t) selected keys ascending (k_t
+// = k_rows[row] capped at k_eff, or k_eff when k_rows is null), then t+1,
+// t+2, ... up to entry k_t - 1 (the lowest-index invalid entries, as the
+// selector orders them; entries below k_t past n exist only when t+1 < k_t,
+// so these stay below k_t <= T), then index 0 in entries k_t .. k_eff - 1
+// (like the adaptive standalone selector's entries past k_t).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void bits_to_indices_kernel(const uint32_t* __restrict__ bits, int64_t b_sb,
                                                               int64_t b_st, int T, int W, int k_eff,
+                                                              const int32_t* __restrict__ k_rows,
                                                               int32_t* __restrict__ idx_out,
                                                               int32_t* __restrict__ count_out) {
   __shared__ int wave_tot[4];
@@ -766,7 +771,8 @@ __global__ __launch_bounds__(256) void bits_to_indices_kernel(const uint32_t* __
     }
   }
   const int n = min(total, k_eff);
-  for (int i = n + tid; i < k_eff; i += 256) orow[i] = t + 1 + (i - n);
+  const int k_row = k_rows ? min(k_rows[row], k_eff) : k_eff;
+  for (int i = n + tid; i < k_eff; i += 256) orow[i] = i < k_row ? t + 1 + (i - n) : 0;
   if (tid == 0) count_out[row] = n;
 }
 
@@ -936,7 +942,7 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
   if (st || !idx_out) return st;
   const int W = 2 * ((T + 63) / 64);
   hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_eff,
-                     idx_out, count_out);
+                     nullptr, idx_out, count_out);
   return launch_status();
 }
 
@@ -994,6 +1000,6 @@ extern "C" int gsa_indexer_select_adaptive(const void* q_idx, int64_t q_sb, int6
   if (st || !idx_out) return st;
   const int W = 2 * ((T + 63) / 64);
   hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_cap,
-                     idx_out, count_out);
+                     krow, idx_out, count_out);
   return launch_status();
 }

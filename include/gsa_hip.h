@@ -158,8 +158,10 @@ int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
  * and row t selects its k_t largest causal scores exactly as gsa_indexer_select
  * does for a fixed k (ties at the k-th value to the lowest indices).
  * Outputs: bits as gsa_indexer_select; optionally idx_out int32
- * [B,T,min(k_max,T)] and count_out int32 [B,T] (count = min(t+1, k_t));
- * optionally k_out int32 [B*T] (k_t) and var_out float [B*T] (var_t).
+ * [B,T,min(k_max,T)] and count_out int32 [B,T] (count = min(t+1, k_t);
+ * row t: the count selected keys ascending, then t+1, t+2, ... up to entry
+ * k_t - 1 (present only when t+1 < k_t), then index 0 up to the width, so
+ * every entry lies in [0, T)); optionally k_out int32 [B*T] (k_t) and var_out float [B*T] (var_t).
  * Three launches on the stream (scores + variances; the global mean and k_t;
  * the select), all in stream order.  ws: at least
  * gsa_indexer_select_adaptive_workspace_bytes(B, T) bytes (16-byte aligned):

@@ -174,6 +174,23 @@ def select_ascending(scores: torch.Tensor, k_eff: int) -> Tuple[torch.Tensor, to
     return out, mask.sum(dim=-1).to(torch.int32)
 
 
+def row_variance(scores: torch.Tensor) -> torch.Tensor:
+    """Population variance of each row's valid (finite) scores (gsa_explained.ipynb:577-592)."""
+    valid = scores != float("-inf")
+    cnt = valid.sum(dim=-1, keepdim=True).clamp(min=1).float()
+    sv = scores.masked_fill(~valid, 0.0)
+    mean = sv.sum(dim=-1, keepdim=True) / cnt
+    diff = (sv - mean * valid.float()).masked_fill(~valid, 0.0)
+    return diff.pow(2).sum(dim=-1) / cnt.squeeze(-1)
+
+
+def adaptive_k_from_variance(var: torch.Tensor, k_base: int, k_min: int, k_max: int) -> torch.Tensor:
+    """k_t = clamp(floor(k_base * avg_var / var_t), k_min, k_max); avg_var = mean of var over every
+    row (and batch); both variances clamped to >= 1e-6 (gsa_explained.ipynb:577-592)."""
+    avg = var.mean().clamp(min=1e-6)
+    return (k_base * avg / var.clamp(min=1e-6)).floor().clamp(min=k_min, max=k_max).long()
+
+
 def adaptive_k(scores: torch.Tensor, k_base: int, k_min: int, k_max: int) -> torch.Tensor:
     """Variance-based per-row k (gsa_explained.ipynb:577-592).
 
@@ -181,14 +198,7 @@ def adaptive_k(scores: torch.Tensor, k_base: int, k_min: int, k_max: int) -> tor
     var over all rows (and batches) is avg_var; k_t = clamp(floor(k_base *
     avg_var / var_t), k_min, k_max), with both variances clamped to >= 1e-6.
     """
-    valid = scores != float("-inf")
-    cnt = valid.sum(dim=-1, keepdim=True).clamp(min=1).float()
-    sv = scores.masked_fill(~valid, 0.0)
-    mean = sv.sum(dim=-1, keepdim=True) / cnt
-    diff = (sv - mean * valid.float()).masked_fill(~valid, 0.0)
-    var = diff.pow(2).sum(dim=-1) / cnt.squeeze(-1)
-    avg = var.mean().clamp(min=1e-6)
-    return (k_base * avg / var.clamp(min=1e-6)).floor().clamp(min=k_min, max=k_max).long()
+    return adaptive_k_from_variance(row_variance(scores), k_base, k_min, k_max)
 
 
 # ---------------------------------------------------------------------------
@@ -298,43 +308,68 @@ def synthetic_input(B: int, T: int, D: int, seed: int = 1,
 
 @dataclass
 class Projections:
-    q: torch.Tensor       # [B,T,H,d] after RoPE
-    k: torch.Tensor       # [B,T,H,d] after RoPE
-    v: torch.Tensor       # [B,T,H,d] after the value gate
-    og: torch.Tensor      # [B,T,D] output-gate sigmoid
-    q_idx: torch.Tensor   # [B,T,Hi,di]
-    k_idx: torch.Tensor   # [B,T,di]
-    w_idx: torch.Tensor   # [B,T,Hi]
+    q: Optional[torch.Tensor]       # [B,T,H,d] after RoPE
+    k: Optional[torch.Tensor]       # [B,T,H,d] after RoPE
+    v: Optional[torch.Tensor]       # [B,T,H,d] after the value gate
+    og: Optional[torch.Tensor]      # [B,T,D] output-gate sigmoid
+    q_idx: Optional[torch.Tensor]   # [B,T,Hi,di]
+    k_idx: Optional[torch.Tensor]   # [B,T,di]
+    w_idx: Optional[torch.Tensor]   # [B,T,Hi]
+
+
+PARTS = ("q", "k", "v", "og", "q_idx", "k_idx", "w_idx")
 
 
 def project(sd: Dict[str, torch.Tensor], cfg: GSAConfig, x: torch.Tensor,
-            rope: Optional[RopeCache] = None) -> Projections:
+            rope: Optional[RopeCache] = None, pos0: int = 0, seq_len: Optional[int] = None,
+            parts=PARTS) -> Projections:
     """Steps 1-3 of gsa_ref.GatedSparseAttention.forward plus the indexer projections.
 
     q,k,v = Linear(x) (gsa_ref.py:283-285); v *= sigmoid(gate_v(x))
     (gsa_ref.py:163-166); RoPE on q,k (gsa_ref.py:295-298); idx_q/idx_k/idx_w
     projections (gsa_ref.py:100-102); sigmoid(gate_o(x)) (gsa_ref.py:178).
+
+    ``x`` may be a row slice of the layer input: its first row sits at
+    absolute position ``pos0`` of a layer call over ``seq_len`` rows (default
+    pos0 + rows), and the RoPE tables are the ones that call requests
+    (gsa_ref.py:293: ``rotary_emb(seq_len)``, which decides the >8192 rebuild)
+    read at those positions.  ``parts`` names the projections to compute; the
+    others are None.
     """
     B, T, D = x.shape
     H, d = cfg.num_heads, cfg.d_head
     dt = x.dtype
+    seq_len = pos0 + T if seq_len is None else seq_len
+    if pos0 < 0 or pos0 + T > seq_len:
+        raise ValueError(f"rows [{pos0}, {pos0 + T}) outside a layer call over {seq_len} rows")
+    unknown = set(parts) - set(PARTS)
+    if unknown:
+        raise ValueError(f"unknown projections {sorted(unknown)}")
     if rope is None:
         rope = RopeCache(d, dt, sd["rotary_emb.inv_freq"])
-    q = F.linear(x, sd["q_proj.weight"]).view(B, T, H, d)
-    k = F.linear(x, sd["k_proj.weight"]).view(B, T, H, d)
-    v = F.linear(x, sd["v_proj.weight"]).view(B, T, H, d)
-    gv = torch.sigmoid(F.linear(x, sd["value_gate.gate_proj.weight"], sd["value_gate.gate_proj.bias"]))
-    v = v * gv.view(B, T, H, d)
-    cos, sin = rope.tables(T, dt)
-    cos = cos.unsqueeze(0).unsqueeze(2)
-    sin = sin.unsqueeze(0).unsqueeze(2)
-    q = apply_rope(q, cos, sin)
-    k = apply_rope(k, cos, sin)
-    og = torch.sigmoid(F.linear(x, sd["output_gate.gate_proj.weight"], sd["output_gate.gate_proj.bias"]))
-    qi = F.linear(x, sd["indexer.idx_q_proj.weight"]).view(B, T, cfg.n_idx_heads, cfg.d_indexer)
-    ki = F.linear(x, sd["indexer.idx_k_proj.weight"])
-    wi = F.linear(x, sd["indexer.idx_w_proj.weight"], sd["indexer.idx_w_proj.bias"])
-    return Projections(q, k, v, og, qi, ki, wi)
+    out = dict.fromkeys(PARTS)
+    if "q" in parts or "k" in parts:
+        cos, sin = rope.tables(seq_len, dt)
+        cos = cos[pos0:pos0 + T].unsqueeze(0).unsqueeze(2)
+        sin = sin[pos0:pos0 + T].unsqueeze(0).unsqueeze(2)
+    if "q" in parts:
+        out["q"] = apply_rope(F.linear(x, sd["q_proj.weight"]).view(B, T, H, d), cos, sin)
+    if "k" in parts:
+        out["k"] = apply_rope(F.linear(x, sd["k_proj.weight"]).view(B, T, H, d), cos, sin)
+    if "v" in parts:
+        v = F.linear(x, sd["v_proj.weight"]).view(B, T, H, d)
+        gv = torch.sigmoid(F.linear(x, sd["value_gate.gate_proj.weight"], sd["value_gate.gate_proj.bias"]))
+        out["v"] = v * gv.view(B, T, H, d)
+    if "og" in parts:
+        out["og"] = torch.sigmoid(F.linear(x, sd["output_gate.gate_proj.weight"],
+                                           sd["output_gate.gate_proj.bias"]))
+    if "q_idx" in parts:
+        out["q_idx"] = F.linear(x, sd["indexer.idx_q_proj.weight"]).view(B, T, cfg.n_idx_heads, cfg.d_indexer)
+    if "k_idx" in parts:
+        out["k_idx"] = F.linear(x, sd["indexer.idx_k_proj.weight"])
+    if "w_idx" in parts:
+        out["w_idx"] = F.linear(x, sd["indexer.idx_w_proj.weight"], sd["indexer.idx_w_proj.bias"])
+    return Projections(**out)
 
 
 def gsa_forward(sd: Dict[str, torch.Tensor], cfg: GSAConfig, x: torch.Tensor,
@@ -359,24 +394,34 @@ def gsa_forward(sd: Dict[str, torch.Tensor], cfg: GSAConfig, x: torch.Tensor,
 
 def attend_rows(sd: Dict[str, torch.Tensor], cfg: GSAConfig, p: Projections,
                 r0: int, r1: int, idx: Optional[torch.Tensor] = None,
-                mask: Optional[torch.Tensor] = None, return_sel: bool = False):
-    """Query rows [r0, r1) of the layer, given all rows' projections.
+                mask: Optional[torch.Tensor] = None, return_sel: bool = False,
+                rows: Optional[Projections] = None):
+    """Query rows [r0, r1) of the layer, given the keys' projections.
 
     Query-chunked form of gsa_ref.py:303-323: the indexer for the chunk uses
-    the absolute-position causal mask of benchmark_models.ipynb:107-115.  With
-    ``idx``/``mask`` given, the selection is taken from them (used to check the
-    attention on the kernel's own indices).  Returns the layer output rows
-    [B, r1-r0, D] (and the selection when asked).
+    the absolute-position causal mask of benchmark_models.ipynb:107-115.  The
+    query-side projections (q, og, q_idx, w_idx) are ``p``'s rows [r0, r1),
+    or ``rows``' when given (``rows`` then holds exactly those rows); k, v
+    and k_idx come from ``p`` for every key.  With ``idx``/``mask`` given,
+    the selection is taken from them (used to check the attention on the
+    kernel's own indices).  Returns the layer output rows [B, r1-r0, D] (and
+    the selection when asked).
     """
-    B, T = p.q.shape[0], p.q.shape[1]
+    B, T = p.k.shape[0], p.k.shape[1]
     D = cfg.hidden_size
+    if rows is None:
+        q, og, q_idx, w_idx = p.q[:, r0:r1], p.og[:, r0:r1], p.q_idx[:, r0:r1], p.w_idx[:, r0:r1]
+    else:
+        q, og, q_idx, w_idx = rows.q, rows.og, rows.q_idx, rows.w_idx
+        if q.shape[1] != r1 - r0:
+            raise ValueError(f"rows holds {q.shape[1]} query rows, expected {r1 - r0}")
     k_eff = k_effective(cfg.k_base, cfg.k_max, T)
     if idx is None:
-        s = indexer_scores(p.q_idx[:, r0:r1], p.k_idx, p.w_idx[:, r0:r1],
-                           sd["indexer.idx_bias"], 1.0 / math.sqrt(cfg.d_indexer), q_offset=r0)
+        s = indexer_scores(q_idx, p.k_idx, w_idx, sd["indexer.idx_bias"], 1.0 / math.sqrt(cfg.d_indexer),
+                           q_offset=r0)
         idx, mask = select_topk(s, k_eff)
-    attn = sparse_attention(p.q[:, r0:r1], p.k, p.v, idx, mask, cfg.scale)
-    attn = attn * p.og[:, r0:r1].view(B, r1 - r0, cfg.num_heads, cfg.d_head)
+    attn = sparse_attention(q, p.k, p.v, idx, mask, cfg.scale)
+    attn = attn * og.view(B, r1 - r0, cfg.num_heads, cfg.d_head)
     out = F.linear(attn.reshape(B, r1 - r0, D), sd["o_proj.weight"])
     if return_sel:
         return out, idx, mask

@@ -202,3 +202,27 @@ def test_layer_variance_mode_vs_oracle(dev, impl):
     _log(f"  bf16 rel-L2 {rel:.3e} max|err| {err.max().item():.3e}")
     assert torch.all(err <= 2e-2 + 1e-2 * ref.abs())
     assert rel < 2e-2
+
+
+def test_indexer_select_adaptive_indices_stay_in_range(dev):
+    """Past its count, row t holds t+1, t+2, ... up to entry k_t - 1 (rows with
+    t+1 < k_t), then index 0 up to the output width: every entry lies in [0, T)."""
+    B, T = 1, 700
+    g = torch.Generator().manual_seed(21)
+    buf = torch.randn(B, T, 324, generator=g).to(torch.bfloat16)
+    sig = torch.linspace(0.2, 3.0, T).view(1, T, 1)
+    q = (buf[..., :256].float() * sig).to(torch.bfloat16).view(B, T, 4, 64)
+    k, w = buf[..., 256:320], buf[..., 320:324]
+    _, idx, cnt, k_rows, _ = _abi.indexer_select_adaptive(q.to(dev), k.to(dev), w.to(dev),
+                                                          torch.zeros(4, device=dev), 0.125, 64, 16, 400)
+    idx, cnt, k_rows = idx.cpu(), cnt.cpu(), k_rows.cpu()
+    assert idx.shape[-1] == 400
+    assert int(idx.min()) >= 0 and int(idx.max()) < T
+    t = torch.arange(T)
+    assert torch.equal(cnt[0].long(), torch.minimum(t + 1, k_rows[0].long()))
+    short = (cnt[0] < 400).nonzero().flatten()
+    assert short.numel() > 0 and bool((k_rows[0, short] < torch.minimum(t[short] + 1, torch.tensor(400))).any())
+    for r in short.tolist():
+        n, kr = int(cnt[0, r]), int(k_rows[0, r])
+        assert idx[0, r, n:kr].tolist() == list(range(r + 1, r + 1 + max(0, kr - n)))
+        assert torch.all(idx[0, r, max(n, kr):] == 0)

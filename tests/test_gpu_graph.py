@@ -70,3 +70,30 @@ def test_graph_refuses_other_shapes_and_rebuilt_weights(dev):
     m.fuse_projections()
     with pytest.raises(RuntimeError):
         g(x)
+
+
+def test_graph_holds_its_rope_tables_and_refuses_after_a_cache_rebuild(dev):
+    """The recorded forward reads its cast RoPE tables by address.  Eager forwards over
+    other row counts cast other tables: replays must still equal the recorded input's
+    eager result, also after those forwards' buffers were freed and the memory was
+    filled with other data.  A forward over more rows than the cache holds rebuilds
+    it (later, shorter calls read the rebuilt tables): the graph then refuses."""
+    m = _model(dev)
+    x = orc.synthetic_input(1, 128, 512, seed=51).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        ref = m(x).clone()
+    g = GraphedForward(m, x)
+    with torch.no_grad():
+        m(orc.synthetic_input(1, 64, 512, seed=52).to(torch.bfloat16).to(dev))   # casts 64-row tables
+        m(orc.synthetic_input(1, 96, 512, seed=53).to(torch.bfloat16).to(dev))   # and 96-row ones
+    junk = [torch.full((1 << 16,), 7.0, device=dev) for _ in range(64)]          # reuse freed memory
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y = g(x).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref)
+    with torch.no_grad():
+        m(orc.synthetic_input(1, 8300, 512, seed=54).to(torch.bfloat16).to(dev))   # rebuilds the cache
+    del junk
+    with pytest.raises(RuntimeError, match="RoPE cache"):
+        g(x)

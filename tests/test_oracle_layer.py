@@ -213,3 +213,29 @@ def test_planted_wiring_mistakes_fail(case, monkeypatch, plant):
     plant(monkeypatch)
     err = _mismatch(sd, x, y, s, sel)
     assert not _ok(err), f"{plant.__name__} went unnoticed: {err}"
+
+
+def test_partial_projection_equals_full_rows():
+    """project(x[:, r0:r1], pos0=r0, seq_len=T) is the full projection's rows, also
+    past the 8192-entry RoPE cache (the call over T rows rebuilds the tables from
+    the bf16 inv_freq, and the slice must read those), and attend_rows with the
+    query rows given separately equals attend_rows on the full projection."""
+    cfg = orc.GSAConfig(hidden_size=256, num_heads=2, k_max=64, k_base=16, k_min=4)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=21), torch.bfloat16)
+    Tn = 8200
+    x = orc.synthetic_input(1, Tn, cfg.hidden_size, seed=22).to(torch.bfloat16)
+    full = orc.project(sd, cfg, x)
+    keys = orc.project(sd, cfg, x, parts=("k", "v", "k_idx"))
+    assert keys.q is None and keys.og is None
+    for r0, r1 in ((0, 40), (8150, 8200)):
+        part = orc.project(sd, cfg, x[:, r0:r1], pos0=r0, seq_len=Tn, parts=("q", "og", "q_idx", "w_idx"))
+        for name in ("q", "og", "q_idx", "w_idx"):
+            assert torch.equal(getattr(part, name), getattr(full, name)[:, r0:r1]), name
+        a = orc.attend_rows(sd, cfg, full, r0, r1)
+        b = orc.attend_rows(sd, cfg, keys, r0, r1, rows=part)
+        assert torch.equal(a, b)
+    # the slice really reads the rebuilt tables: a call over r1 rows only (no rebuild) differs
+    short = orc.project(sd, cfg, x[:, 8150:8190], pos0=8150, seq_len=8190, parts=("q",))
+    assert not torch.equal(short.q, full.q[:, 8150:8190])
+    with pytest.raises(ValueError):
+        orc.project(sd, cfg, x[:, :10], pos0=Tn - 5, seq_len=Tn)
