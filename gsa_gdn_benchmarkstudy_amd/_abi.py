@@ -38,7 +38,7 @@ EXPORTS = (
     "gsa_indexer_select_workspace_bytes", "gsa_indexer_select_adaptive",
     "gsa_indexer_select_adaptive_workspace_bytes", "gsa_topk_select_adaptive",
     "gsa_proj_packed_bytes", "gsa_proj_pack", "gsa_proj_fused", "gsa_dense_lane_masks",
-    "gsa_prologue_vt_lane_masks",
+    "gsa_prologue_vt_lane_masks", "gsa_debug_force_select_fallback",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -60,6 +60,7 @@ _PROTOS = {
                                      _vp, _i64, _i64, _vp, _vp, _vp, _vp,
                                      _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_indexer_select_adaptive_workspace_bytes": ([_i32, _i32], ctypes.c_size_t),
+    "gsa_debug_force_select_fallback": ([_i32], _i32),
     "gsa_prologue": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
                       _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
     "gsa_sparse_attn": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
@@ -264,6 +265,19 @@ def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int, indices: b
                                 _ptr(ws), nbytes, _stream(q_idx))
     _check(st, "gsa_indexer_select")
     return bits, idx, cnt
+
+
+class forced_select_fallback:
+    """Context manager: the fused selector's rows take its exact fallback path
+    (gsa_debug_force_select_fallback; a test hook)."""
+
+    def __enter__(self):
+        self._prev = load().gsa_debug_force_select_fallback(1)
+        return self
+
+    def __exit__(self, *exc):
+        load().gsa_debug_force_select_fallback(self._prev)
+        return False
 
 
 def indexer_select_adaptive_workspace_bytes(B: int, T: int) -> int:

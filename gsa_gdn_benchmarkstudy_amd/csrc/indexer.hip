@@ -5,15 +5,17 @@
 // (semantics of gsa_triton/gsa_ref.py:97-126).  Both kernels below share one
 // score routine -- the same MFMA sequence and the same epilogue instructions
 // -- so a score is bit-identical wherever it is computed; the fused selector
-// relies on that to recompute scores pass after pass.
+// relies on that when it recomputes scores pass after pass.
 //
-// Tiling: one wave owns 16 query rows.  Its MFMA A operand (q, 4 heads x 64
-// dims) stays in registers for the whole kernel; keys stream through in tiles
-// of 16, each tile one 16x16 output block per head:
+// Tiling: one wave owns 16 query rows.  The product is taken transposed,
+// D = K Q^T: the MFMA A operand is a tile of 16 keys (streamed), the B
+// operand the wave's 16 query rows (4 heads x 64 dims, in registers for the
+// whole kernel):
 //   bf16: v_mfma_f32_16x16x32_bf16, 2 k-steps per head  (8 MFMA per tile)
 //   fp32: v_mfma_f32_16x16x4_f32,  16 k-steps per head (64 MFMA per tile)
-// Output layout of a 16x16 block: lane l holds rows 4*(l/16)+e (e = 0..3) of
-// column l%16.
+// Output layout of a 16x16 block: lane l holds rows 4*(l/16)+e (e = 0..3)
+// of column l%16, i.e. query row r0 + l%16 against the four consecutive keys
+// j0 + 4*(l/16) + e.  Every per-row quantity is therefore lane-local.
 #include "gsa_common.h"
 
 #pragma clang fp contract(off)
@@ -57,11 +59,13 @@ struct IdxArgs {
   int B, T;
 };
 
-// Per-lane state of one wave's 16-row group.
+// Per-lane state of one wave's 16-row group: lane l works for query row
+// r0 + l%16.
 template <typename T>
 struct RowGroup {
-  typename Mfma<T>::Op qa[kHi][Mfma<T>::kSteps];  // A operand: row r0 + lane%16
-  float a[4][kHi];                                // sigmoid(w) of rows r0 + 4*(lane/16) + e
+  typename Mfma<T>::Op qb[kHi][Mfma<T>::kSteps];  // B operand: query row r0 + lane%16
+  float a[kHi];                                   // sigmoid(w) of the lane's row
+  float c01, c23;                                 // a0 + a1, a2 + a3
   float bias_l2[kHi];                             // -bias[h] * log2(e)
   float scale_l2;                                 // -scale * log2(e)
   const T* kbase;                                 // k_idx of this batch
@@ -69,26 +73,23 @@ struct RowGroup {
 
   __device__ void init(const IdxArgs& p, int b, int r0, int lane) {
     const int g = lane >> 4, lr = lane & 15;
-    const T* qb = static_cast<const T*>(p.q) + b * p.q_sb;
-    const int qrow = min(r0 + lr, p.T - 1);
-    const T* qrp = qb + (int64_t)qrow * p.q_st;
+    const int row = min(r0 + lr, p.T - 1);
+    const T* qrp = static_cast<const T*>(p.q) + b * p.q_sb + (int64_t)row * p.q_st;
 #pragma unroll
     for (int h = 0; h < kHi; ++h)
 #pragma unroll
-      for (int s = 0; s < Mfma<T>::kSteps; ++s) qa[h][s] = Mfma<T>::load(qrp, h * kDi, s, g);
-    const T* wb = static_cast<const T*>(p.w) + b * p.w_sb;
+      for (int s = 0; s < Mfma<T>::kSteps; ++s) qb[h][s] = Mfma<T>::load(qrp, h * kDi, s, g);
+    const T* wrp = static_cast<const T*>(p.w) + b * p.w_sb + (int64_t)row * p.w_st;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = min(r0 + 4 * g + e, p.T - 1);
-#pragma unroll
-      for (int h = 0; h < kHi; ++h) {
-        const T wv = wb[(int64_t)row * p.w_st + h];
-        float wf;
-        if constexpr (Elem<T>::kBf16) wf = __uint_as_float((uint32_t)wv << 16);
-        else wf = wv;
-        a[e][h] = sigmoidf_fast(wf);
-      }
+    for (int h = 0; h < kHi; ++h) {
+      const T wv = wrp[h];
+      float wf;
+      if constexpr (Elem<T>::kBf16) wf = __uint_as_float((uint32_t)wv << 16);
+      else wf = wv;
+      a[h] = sigmoidf_fast(wf);
     }
+    c01 = a[0] + a[1];
+    c23 = a[2] + a[3];
     kbase = static_cast<const T*>(p.k) + b * p.k_sb;
     k_st = p.k_st;
 #pragma unroll
@@ -96,7 +97,7 @@ struct RowGroup {
     scale_l2 = p.scale_l2;
   }
 
-  // B operand of key tile [j0, j0+16): column lane%16, clamped to a valid row.
+  // A operand of key tile [j0, j0+16): key j0 + lane%16, clamped to a valid row.
   __device__ void load_keys(int j0, int T_, int lane, typename Mfma<T>::Op (&kb)[Mfma<T>::kSteps]) const {
     const int j = min(j0 + (lane & 15), T_ - 1);
     const T* krp = kbase + (int64_t)j * k_st;
@@ -109,19 +110,36 @@ struct RowGroup {
     for (int h = 0; h < kHi; ++h) {
       floatx4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < Mfma<T>::kSteps; ++s) c = Mfma<T>::mma(qa[h][s], kb[s], c);
+      for (int s = 0; s < Mfma<T>::kSteps; ++s) c = Mfma<T>::mma(kb[s], qb[h][s], c);
       acc[h] = c;
     }
   }
 
-  // Fused epilogue for output slot e: sum_h a_h * sigmoid(scale*dot_h + bias_h).
+  // Fused epilogue for slot e: sum_h a_h * sigmoid(scale*dot_h + bias_h).
+  // With x_h = 2^(-(scale*dot_h + bias_h) log2 e), sigmoid = 1/(1 + x_h), and
+  // the four terms are summed over one common denominator,
+  //   a0/(1+x0) + a1/(1+x1) = (a0 + a1 + a0 x1 + a1 x0) / ((1+x0)(1+x1)),
+  // the two pairs likewise: 4 exp2 and 1 reciprocal instead of 4 + 4.  Every
+  // term is positive, so nothing cancels; the result is within a few fp32
+  // ulps of the per-head form.  When the common denominator leaves the
+  // range where numerator and denominator are finite (some x_h beyond about
+  // 2^31, or a non-finite input), the per-head form runs instead.
   __device__ float score(const floatx4 (&acc)[kHi], int e) const {
-    float s = 0.f;
+    float x[kHi];
 #pragma unroll
-    for (int h = 0; h < kHi; ++h) {
-      const float t = __builtin_fmaf(acc[h][e], scale_l2, bias_l2[h]);
-      const float r = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
-      s = (h == 0) ? a[e][h] * r : __builtin_fmaf(a[e][h], r, s);
+    for (int h = 0; h < kHi; ++h) x[h] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[h][e], scale_l2, bias_l2[h]));
+    const float u0 = 1.0f + x[0], u2 = 1.0f + x[2];
+    const float d01 = __builtin_fmaf(u0, x[1], u0);     // (1+x0)(1+x1)
+    const float d23 = __builtin_fmaf(u2, x[3], u2);
+    const float n01 = __builtin_fmaf(a[1], x[0], __builtin_fmaf(a[0], x[1], c01));
+    const float n23 = __builtin_fmaf(a[3], x[2], __builtin_fmaf(a[2], x[3], c23));
+    const float den = d01 * d23;
+    const float num = __builtin_fmaf(n01, d23, n23 * d01);
+    float s = num * __builtin_amdgcn_rcpf(den);
+    if (!(den < 0x1p124f)) {     // also NaN
+      s = a[0] * __builtin_amdgcn_rcpf(1.0f + x[0]);
+#pragma unroll
+      for (int h = 1; h < kHi; ++h) s = __builtin_fmaf(a[h], __builtin_amdgcn_rcpf(1.0f + x[h]), s);
     }
     return s;
   }
@@ -130,11 +148,12 @@ struct RowGroup {
 // ---------------------------------------------------------------------------
 // Full score matrix (the fused_gated_indexer API).  4 waves per block, one
 // 16-row group per wave; causal tiles above the diagonal are filled with -inf
-// without computing them.
+// without computing them.  A lane writes its row's four consecutive keys of
+// a tile with one 16-byte store when `vec` (scores, s_sb and s_st allow it).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int causal, float* S,
-                                                             int64_t s_sb, int64_t s_st) {
+                                                             int64_t s_sb, int64_t s_st, int vec) {
   const int lane = threadIdx.x & 63;
   const int ngroups = (p.T + 15) >> 4;
   const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -142,10 +161,21 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
   const int b = wv / ngroups;
   const int r0 = (wv % ngroups) * 16;
   const int g = lane >> 4, lr = lane & 15;
+  const int row = r0 + lr;
 
   RowGroup<T> rg;
   rg.init(p, b, r0, lane);
-  float* Sb = S + b * s_sb;
+  float* srow = S + b * s_sb + (int64_t)min(row, p.T - 1) * s_st;
+  auto put = [&](int col0, const float (&v)[4]) {
+    if (row >= p.T) return;
+    if (vec && col0 + 3 < p.T) {
+      *reinterpret_cast<floatx4*>(srow + col0) = floatx4{v[0], v[1], v[2], v[3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (col0 + e < p.T) srow[col0 + e] = v[e];
+    }
+  };
 
   const int jend = causal ? min(p.T, r0 + 16) : p.T;
   typename Mfma<T>::Op kb[Mfma<T>::kSteps], kn[Mfma<T>::kSteps];
@@ -156,91 +186,87 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
     if (j0 + 16 < jend) rg.load_keys(j0 + 16, p.T, lane, kn);
     floatx4 acc[kHi];
     rg.mma(kb, acc);
-    const int col = j0 + lr;
+    const int col0 = j0 + 4 * g;
+    float v[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = r0 + 4 * g + e;
-      if (row < p.T && col < p.T) {
-        const float sc = (causal && col > row) ? -__builtin_inff() : rg.score(acc, e);
-        Sb[(int64_t)row * s_st + col] = sc;
-      }
-    }
+    for (int e = 0; e < 4; ++e) v[e] = (causal && col0 + e > row) ? -__builtin_inff() : rg.score(acc, e);
+    put(col0, v);
   }
-  for (int j0 = ((jend + 15) >> 4) << 4; j0 < p.T; j0 += 16) {
-    const int col = j0 + lr;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = r0 + 4 * g + e;
-      if (row < p.T && col < p.T) Sb[(int64_t)row * s_st + col] = -__builtin_inff();
-    }
-  }
+  const float ninf[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  for (int j0 = ((jend + 15) >> 4) << 4; j0 < p.T; j0 += 16) put(j0 + 4 * g, ninf);
 }
-
 // ---------------------------------------------------------------------------
 // Fused indexer + exact top-k.
 //
 // Output: the selection as a bitmask, bits[b][t] bit j set iff key j is one
 // of row t's selected keys (W = 2*ceil(T/64) uint32 words per row; words past
-// row t's causal range are zero).  One 512-thread block per 16-row group,
-// heaviest groups first; its 8 waves take the group's causal 16-key tiles
-// round-robin and share the row state in LDS (8 rather than 4 waves halve
-// the time of the heaviest groups, which bound the kernel when the whole
-// grid fits the GPU at once).  Rows with t+1 <= k select
-// every causal key.  For the others:
-//   pass 1  MFMA scores -> value-linear histogram, bin = floor(s * NB /
-//           sum_h sigmoid(w_h)), and every score tile is stored to the
-//           workspace -> the bin b1 holding the k-th largest score and the
-//           rank of the k-th largest inside it;
-//   pass 2  the stored scores are read back: entries in bins above b1 are
-//           selected (ballots -> one 64-bit word of the row's bitmask per 4
-//           tiles); entries in b1 (at most kWCap per row and wave) are
-//           collected as (key, index);
-//   resolve exact MSB-first radix select among a row's candidates -> the
-//           threshold key theta and how many entries equal to theta to take,
-//           lowest indices first; winning candidates are OR-ed into the mask.
-// A bin holding more candidates than fit (degenerate scores, e.g. all equal)
-// falls back to four 8-bit radix passes over the stored scores of the bin,
-// then one ordered pass by a single wave marks the winners.
+// row t's causal range are zero).  One 1024-thread block (16 waves) per
+// 16-row group, heaviest groups first; the waves share the group's causal
+// 16-key tiles.  Rows with t+1 <= k select every causal key.  For the
+// others, no score is ever stored:
+//   sample  exact scores of every fourth tile (the first of each 64-key
+//           quad) -> a value-linear histogram per row, bin = floor(s * NB /
+//           sum_h sigmoid(w_h)) -> a band [lo, hi] around the k-th largest
+//           score: the sample ranks k*n_s/n -+ (z*sigma + 2), sigma the
+//           standard deviation of the sample count above a population
+//           quantile (hypergeometric), z = 5;
+//   main    exact scores of every tile: s > hi (or NaN) is a sure winner and
+//           goes straight into the row's 64-bit mask word (one store per
+//           quad); lo <= s <= hi is a candidate, appended as (key, index)
+//           to the row's list in LDS; below lo is dropped;
+//   resolve a row is proven exact when n_sure <= k <= n_sure + n_cand (the
+//           k best in (score desc, index asc) order are then the sure ones and
+//           the first k - n_sure candidates in that order): one wave per row
+//           radix-selects the threshold key among the candidates with 8-bit
+//           digit histograms, breaks ties at it by lowest index, and ORs the
+//           winners into the mask;
+//   fallback  a row that fails the check (the band missed -- about 6e-7 per
+//           row on independent scores -- its list overflowed, or degenerate
+//           scores put the whole row in the band) is selected by an exact
+//           radix select over recomputed scores: four 8-bit digit passes of
+//           the score key, two digit passes of the index among ties at the
+//           threshold, then one marking pass that rewrites the row's words.
 //
-// Workspace: group g of batch b owns (g+1) consecutive 1 KiB score tiles
-// starting at tile b*tri(G) + tri(g), tri(n) = n(n+1)/2, G = ceil(T/16);
-// lane l of the wave that computes a tile stores its four output slots
-// (rows 4*(l/16)+e, column l%16) as floats 4l .. 4l+3, the layout it reads
-// back.  After the score tiles, block i owns 16 x kCap (key, index) slots
-// for its rows' candidates (kept out of LDS, so that a block needs only its
-// 17 KiB of histograms and can share a CU with a GEMM block).
+// Memory order.  On gfx950 vector loads and stores share one completion
+// counter, which the compiler's waits count in issue order: a wait for a
+// prefetched key tile also waits for any store issued after it on some path
+// that the compiler cannot count.  So the tile loops issue a fixed number of
+// vector memory instructions per tile -- key loads two tiles ahead,
+// unconditional (clamped to the last tile), and one unconditional mask-word
+// store per quad (lanes with nothing to write store to a scratch slot) --
+// and the candidate lists, the only data-dependent writes, live in LDS.
 // ---------------------------------------------------------------------------
-constexpr int kNB = 512;                 // histogram bins per row
-constexpr int kGroupWaves = 8;           // waves per 16-row group
+constexpr int kNB = 1024;                 // sample histogram bins per row
+constexpr int kHStride = kNB / 2 + 1;     // words per row: 16-bit counts, two per word, + trash bin kNB
+constexpr int kGroupWaves = 16;           // waves per 16-row group
 constexpr int kGroupThreads = 64 * kGroupWaves;
-constexpr int kWCap = 128;               // candidates per row and wave
-constexpr int kCap = kWCap * kGroupWaves;  // candidates per row
+constexpr int kRowCap = 1152;             // candidates per row (LDS)
+constexpr float kBandZ = 5.f;             // band half-width in standard deviations of the sample rank
+constexpr int kFbStride = 512;            // fallback digit histograms: 16 rows x 512 words
+// LDS words shared by the phases: the sample histograms (16 x kHStride), the
+// candidate keys (16 x kRowCap u32) and positions (16 x kRowCap u16), the
+// fallback's digit histograms (16 x kFbStride).
+constexpr int kPoolWords = 16 * kRowCap + 8 * kRowCap;
+static_assert(16 * kHStride <= kPoolWords && 16 * kFbStride <= kPoolWords, "LDS pool too small");
+constexpr size_t kPoolBytes = (size_t)kPoolWords * 4;
+constexpr size_t kScratchBytes = 64 * 8;  // per 16-row group: the mask-word store slots of non-writing lanes
+// A candidate's key index is kept in 16 bits (and the 16-bit sample counts
+// hold at most 16 * ceil(T/64) keys per row).
+constexpr int kMaxSelectT = 65536;
 
-// Per-row histogram in LDS.  Packed: 512 bins as 16-bit counts, two per
-// word (exact while a row has at most 65535 keys, i.e. T <= 65535), 17 KiB
-// for the block -- small enough for a block to share a CU with the
-// projection GEMM's.  Unpacked: 32-bit counts.  Bin kNB is a trash bin
-// (invalid slots) in the row's padding word, which no scan reads; the odd
-// row strides put one bin of the 16 rows in distinct banks.  The overflow
-// path's 256-bin digit histograms use 32-bit words with either stride.
-template <bool kPacked>
-struct Hist {
-  static constexpr int kStride = kPacked ? kNB / 2 + 1 : kNB + 1;
-  __device__ static void add(uint32_t* row, int bin) {
-    if constexpr (kPacked) atomicAdd(&row[bin >> 1], 1u << (16 * (bin & 1)));
-    else atomicAdd(&row[bin], 1u);
-  }
-  __device__ static int count(const uint32_t* row, int bin) {
-    if constexpr (kPacked) return (int)((row[bin >> 1] >> (16 * (bin & 1))) & 0xffffu);
-    else return (int)row[bin];
-  }
-};
-constexpr int kTile = 256;               // floats per stored 16x16 score tile
+enum RowMode : int { kNone = 0, kTrivial = 1, kActive = 2, kFailed = 3 };
 
-enum RowMode : int { kNone = 0, kTrivial = 1, kActive = 2, kResolved = 3, kOverflow = 4 };
+// s_waitcnt immediate (gfx9 encoding): vmcnt(0), expcnt and lgkmcnt not waited.
+constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xf << 8);
 
 __device__ __forceinline__ int bin_of(float s, float inv_w) {
   return (int)fmaxf(0.f, fminf(s * inv_w, (float)(kNB - 1)));
+}
+__device__ __forceinline__ void hist_add(uint32_t* row, int bin) {
+  atomicAdd(&row[bin >> 1], 1u << (16 * (bin & 1)));
+}
+__device__ __forceinline__ int hist_count(const uint32_t* row, int bin) {
+  return (int)((row[bin >> 1] >> (16 * (bin & 1))) & 0xffffu);
 }
 
 // Causal-prefix chunk of row `row` for 16-key tile `tile`: keys <= row set.
@@ -249,33 +275,88 @@ __device__ __forceinline__ uint16_t prefix_chunk(int row, int tile) {
   return n >= 16 ? (uint16_t)0xffffu : (n <= 0 ? (uint16_t)0 : (uint16_t)((1u << n) - 1u));
 }
 
+// OR over the four lanes l, l^16, l^32, l^48 (one query row's four key
+// quarters): permlane swaps of the value with itself leave the value and its
+// partner in the two results.
+__device__ __forceinline__ uint32_t or_row4(uint32_t x) {
+  auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = r[0] | r[1];
+  r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return r[0] | r[1];
+}
+__device__ __forceinline__ int wave_min(int v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// Inclusive suffix sum over the lanes: lane l gets sum_{l' >= l} v_l'.
+__device__ __forceinline__ int wave_suffix(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_down(v, o, 64);
+    if (lane + o < 64) v += y;
+  }
+  return v;
+}
+// The lanes of one wave exchange counts through LDS in the resolve, without
+// a workgroup barrier.  Without a fence the compiler may treat another lane's
+// LDS write as invisible and forward a lane's own earlier store to its load
+// (it did: lanes that added nothing read back the zeros they had written).
+// This makes every lane's LDS writes before it visible to every lane's reads
+// after it.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Inclusive prefix sum over the lanes.
+__device__ __forceinline__ int wave_prefix(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(v, o, 64);
+    if (lane >= o) v += y;
+  }
+  return v;
+}
+
 // Selection parameters of one launch.  The kernel runs in one of three phases:
 //   0  fused: every row takes k = k_eff (the reference selector);
-//   1  variance-adaptive k, first launch: pass 1 only, then each row's
-//      population variance of its causal scores -> row_var, and the block's
-//      histograms -> hist (scores stay in the workspace);
+//   1  variance-adaptive k, first launch: the sample histograms -> hist and a
+//      shift per row (the sample mean), then one pass over every causal score
+//      -> each row's population variance -> row_var;
 //   2  variance-adaptive k, second launch: row t takes k = k_rows[b*T+t]; the
-//      histograms come back from hist instead of pass 1, then pass 2,
-//      resolve and overflow as in phase 0.
+//      sample histograms come back from hist, then band, main pass, resolve
+//      and fallback as in phase 0.
 // k_rows is written between the two launches by adaptive_k_kernel, which
 // needs every row's variance (its mean over all rows is global).
 struct SelArgs {
   int k_eff;              // phase 0
   const int* k_rows;      // phase 2: [B*T]
   float* row_var;         // phase 1: [B*T]
-  uint32_t* hist;         // phases 1, 2: 16 * Hist::kStride words per block
+  uint32_t* hist;         // phases 1, 2: 16 * kHStride words per block
+  int force_fallback;     // phases 0, 2: every active row takes the fallback (a test hook)
 };
 
-template <typename T, bool kPacked, int kPhase>
-__global__ __launch_bounds__(kGroupThreads) void indexer_bits_kernel(IdxArgs p, SelArgs sa, uint32_t* bits,
-                                                           int64_t b_sb, int64_t b_st, float* ws, uint2* ws_cand) {
-  using H = Hist<kPacked>;
-  constexpr int kHStride = H::kStride;
-  __shared__ uint32_t sh[16 * kHStride];   // histograms
-  __shared__ uint32_t sh_wcnt[16 * kGroupWaves];
-  __shared__ int st_mode[16], st_b1[16], st_need[16];
-  __shared__ uint32_t st_key[16];
-  __shared__ int st_any[2];                // [0] any active row, [1] any overflow
+template <typename T, int kPhase>
+__global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p, SelArgs sa, uint32_t* bits,
+                                                                     int64_t b_sb, int64_t b_st, uint8_t* ws) {
+  // histograms | candidate lists | fallback histograms: kPoolWords words of
+  // dynamic LDS (more than the 64 KiB a block gets by default, so the launch
+  // raises the block's limit first)
+  extern __shared__ uint32_t pool[];
+  __shared__ uint32_t sh_rh[kGroupWaves][256];    // resolve: one digit histogram per wave
+  __shared__ int st_mode[16], st_k[16], st_need[16], st_ties[16];
+  __shared__ float st_lo[16], st_hi[16], st_invw[16];
+  __shared__ int st_sure[16 * kGroupWaves];
+  __shared__ uint32_t st_cnt[16];
+  __shared__ uint32_t st_key[16], st_idx[16];
+  __shared__ int st_any[3];                       // any active row, any failed row, any index pass
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, lr = lane & 15;
@@ -283,45 +364,48 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_bits_kernel(IdxArgs p, 
   const int b = blockIdx.x % p.B;
   const int rg_idx = ngroups - 1 - blockIdx.x / p.B;
   const int r0 = rg_idx * 16;
+  const int row = r0 + lr;                        // the lane's query row
   uint32_t* bbase = bits + b * b_sb;
   uint16_t* b16 = reinterpret_cast<uint16_t*>(bbase);
-  const int64_t row16 = 2 * b_st;          // uint16 chunks per row
-  float* wsg = ws + ((int64_t)b * ngroups * (ngroups + 1) / 2 + (int64_t)rg_idx * (rg_idx + 1) / 2) * kTile;
-  // this block's candidates (key, index): row rl, wave w, slot i at [rl][w * kWCap + i]
-  uint2* cand = ws_cand + (int64_t)blockIdx.x * 16 * kCap;
+  const int64_t row16 = 2 * b_st;                 // uint16 chunks per row
+  const int ntl = rg_idx + 1;                     // causal 16-key tiles 0 .. rg_idx
+  uint32_t* ckey = pool;                          // [16][kRowCap]
+  uint16_t* cpos = reinterpret_cast<uint16_t*>(pool + 16 * kRowCap);   // [16][kRowCap]
+  // where a lane's mask word goes: its row's word, or a scratch slot
+  uint2* scratch = reinterpret_cast<uint2*>(ws + (int64_t)blockIdx.x * kScratchBytes) + lane;
 
   if (tid < 16) {
-    const int row = r0 + tid;
+    const int r = r0 + tid;
     int k = sa.k_eff;
-    if constexpr (kPhase == 2) k = row < p.T ? sa.k_rows[(int64_t)b * p.T + row] : 1;
+    if constexpr (kPhase == 2) k = r < p.T ? sa.k_rows[(int64_t)b * p.T + r] : 1;
     // phase 1 scores every row (each row's variance enters the global mean)
-    st_mode[tid] = row >= p.T ? kNone : ((kPhase == 1 || row + 1 > k) ? kActive : kTrivial);
-    st_need[tid] = k;
+    st_mode[tid] = r >= p.T ? kNone : ((kPhase == 1 || r + 1 > k) ? kActive : kTrivial);
+    st_k[tid] = k;
+    st_cnt[tid] = 0u;
   }
-  if (tid < 2) st_any[tid] = 0;
+  if (tid < 3) st_any[tid] = 0;
   __syncthreads();
   if (tid < 16 && st_mode[tid] == kActive) st_any[0] = 1;
 
   // Every chunk after the diagonal tile is zero; trivial rows get their
   // causal prefix now.  (The zeroing is largest for the lightest groups.)
   // Phase 1 writes no mask.
-  const int ntl = rg_idx + 1;                  // causal 16-key tiles 0 .. rg_idx
-  const int zend = (rg_idx | 3) + 1;           // chunks up to the end of the 64-key tile
+  const int zend = (rg_idx | 3) + 1;              // chunks up to the end of the 64-key word
   if (kPhase != 1) {
     for (int i = tid; i < 16 * zend; i += kGroupThreads) {
       const int rl = i / zend, tile = i % zend;
-      const int row = r0 + rl;
-      if (row >= p.T) continue;
-      if (tile >= ntl) b16[row * row16 + tile] = 0;
-      else if (st_mode[rl] == kTrivial) b16[row * row16 + tile] = prefix_chunk(row, tile);
+      const int r = r0 + rl;
+      if (r >= p.T) continue;
+      if (tile >= ntl) b16[r * row16 + tile] = 0;
+      else if (st_mode[rl] == kTrivial) b16[r * row16 + tile] = prefix_chunk(r, tile);
     }
     const int W = 2 * ((p.T + 63) >> 6);
-    const int d0 = zend >> 2;                    // first 8-byte pair of words past the 64-key tile
+    const int d0 = zend >> 2;                     // first 8-byte pair of words past the 64-key word
     const int npair = (W >> 1) - d0;
     for (int i = tid; i < 16 * npair; i += kGroupThreads) {
       const int rl = i / npair, pr = d0 + i % npair;
-      const int row = r0 + rl;
-      if (row < p.T) reinterpret_cast<uint2*>(bbase + (int64_t)row * b_st)[pr] = uint2{0u, 0u};
+      const int r = r0 + rl;
+      if (r < p.T) reinterpret_cast<uint2*>(bbase + (int64_t)r * b_st)[pr] = uint2{0u, 0u};
     }
   }
   __syncthreads();
@@ -329,178 +413,101 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_bits_kernel(IdxArgs p, 
 
   RowGroup<T> rgp;
   rgp.init(p, b, r0, lane);
-  bool act[4];
-  int b1[4];
-  float inv_w[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    act[e] = st_mode[4 * g + e] == kActive;
-    const float smax = ((rgp.a[e][0] + rgp.a[e][1]) + rgp.a[e][2]) + rgp.a[e][3];
-    inv_w[e] = (float)kNB / (smax * 1.0009765625f + 1e-30f);
-    b1[e] = 0;
-  }
-  // Lane 16g+e (e < 4) writes the mask chunks of row 4g+e.
-  const int own_row = r0 + 4 * g + (lr & 3);
-  const bool own_act = lr < 4 && st_mode[4 * g + (lr & 3)] == kActive;
-  auto slot_valid = [&](int col, bool (&valid)[4]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) valid[e] = act[e] && col <= r0 + 4 * g + e;
-  };
+  const bool act = st_mode[lr] == kActive;
+  const float inv_w = (float)kNB / ((((rgp.a[0] + rgp.a[1]) + rgp.a[2]) + rgp.a[3]) * 1.0009765625f + 1e-30f);
+  if (wave == 0 && g == 0) st_invw[lr] = inv_w;
+  uint32_t* hrow = pool + lr * kHStride;
+  typedef typename Mfma<T>::Op Op;
+  constexpr int kS = Mfma<T>::kSteps;
 
-  // ---- pass 1: scores -> histogram + workspace ------------------------------
-  // This wave's tiles: wave, wave+4, ...  Scores are computed for every slot
-  // (no divergent branch around the epilogue); invalid slots count into bin
-  // kNB, the row's padding slot, which no scan reads.
-  auto scan_row = [&](int rl, int& nd) -> int {     // top-down cumulative search
-    int cum = 0, bsel = 0;
-    for (int bin = kNB - 1; bin >= 0; --bin) {
-      const int c = H::count(&sh[rl * kHStride], bin);
-      if (cum + c >= nd) { bsel = bin; break; }
-      cum += c;
+  // Scores of the lane's row against keys 16t + 4g + e of the tiles t =
+  // first, next(first), ... below ntl: f(t, s[4]) per tile.  Two key buffers
+  // alternate without copies (the loop handles two tiles per turn): the next
+  // tile's keys are requested before this tile's are awaited, always
+  // (clamped to the last tile), so that the wait is a fixed count that leaves
+  // the new request in flight.
+  auto tile = [&](const Op (&kb)[kS], float (&sc)[4]) {
+    floatx4 acc[kHi];
+    rgp.mma(kb, acc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sc[e] = rgp.score(acc, e);
+  };
+  auto sweep = [&](int first, auto&& next, auto&& f) {
+    Op ka[kS], kb[kS];
+    int t = first;
+    rgp.load_keys(16 * min(t, ntl - 1), p.T, lane, ka);
+    while (t < ntl) {
+      float sc[4];
+      const int t1 = next(t);
+      rgp.load_keys(16 * min(t1, ntl - 1), p.T, lane, kb);
+      tile(ka, sc);
+      f(t, sc);
+      if (t1 >= ntl) break;
+      const int t2 = next(t1);
+      rgp.load_keys(16 * min(t2, ntl - 1), p.T, lane, ka);
+      tile(kb, sc);
+      f(t1, sc);
+      t = t2;
     }
-    nd -= cum;
-    return bsel;
   };
-  auto zero_hist = [&]() {
-    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) sh[i] = 0u;
-    __syncthreads();
-  };
+  auto round_robin = [](int t) { return t + kGroupWaves; };
 
+  // ---- sample histograms -------------------------------------------------------
   if constexpr (kPhase == 2) {
-    // histograms of phase 1 (same grid, so the same block index)
+    // phase 1's histograms (same grid, so the same block index)
     const uint32_t* hsrc = sa.hist + (int64_t)blockIdx.x * (16 * kHStride);
-    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) sh[i] = hsrc[i];
+    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) pool[i] = hsrc[i];
   } else {
-    zero_hist();
-    {
-      typename Mfma<T>::Op kb[Mfma<T>::kSteps], kn[Mfma<T>::kSteps];
-      int t = wave;
-      if (t < ntl) rgp.load_keys(t * 16, p.T, lane, kn);
-      for (; t < ntl; t += kGroupWaves) {
+    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) pool[i] = 0u;
+    __syncthreads();
+    sweep(4 * wave, [](int t) { return t + 4 * kGroupWaves; }, [&](int t, const float (&sc)[4]) {
 #pragma unroll
-        for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = kn[s];
-        if (t + kGroupWaves < ntl) rgp.load_keys((t + kGroupWaves) * 16, p.T, lane, kn);
-        floatx4 acc[kHi];
-        rgp.mma(kb, acc);
-        bool valid[4];
-        slot_valid(t * 16 + lr, valid);
-        floatx4 sc;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sc[e] = rgp.score(acc, e);
-          const int bn = valid[e] ? bin_of(sc[e], inv_w[e]) : kNB;
-          H::add(&sh[(4 * g + e) * kHStride], bn);
-        }
-        *reinterpret_cast<floatx4*>(wsg + t * kTile + lane * 4) = sc;
+      for (int e = 0; e < 4; ++e) {
+        const bool valid = act && 16 * t + 4 * g + e <= row;
+        hist_add(hrow, valid ? bin_of(sc[e], inv_w) : kNB);
       }
-    }
+    });
   }
   __syncthreads();
-  if (kPhase != 1 && tid < 16 && st_mode[tid] == kActive) {
-    int nd = st_need[tid];
-    st_b1[tid] = scan_row(tid, nd);
-    st_need[tid] = nd;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int e = 0; e < 4; ++e) b1[e] = st_b1[4 * g + e];
-
-  // Replay of the stored tiles in quads of 4 consecutive tiles (quad j =
-  // tiles 4j .. 4j+3, one 64-key word pair of the mask).  Each wave takes
-  // runs of kRun consecutive quads, runs round-robin over the waves, and
-  // issues all loads of a run before using any: nothing loaded stays live
-  // across an iteration, so the waits before each quad count only the loads
-  // issued after it.  Tile indices past the last tile re-read the last one
-  // (always in bounds) and every quad of a run is processed: a tile past the
-  // diagonal has no valid slot (its columns lie after every row of the
-  // group), so a quad j >= nquad contributes nothing, and fq must not store
-  // for it.
-  constexpr int kRun = 3;
-  const int nquad = (ntl + 3) >> 2;
-  auto load_quad = [&](int j, floatx4 (&v)[4]) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = min(4 * j + u, ntl - 1);
-      v[u] = *reinterpret_cast<const floatx4*>(wsg + t * kTile + lane * 4);
-    }
-  };
-  // f(quad, u, col, valid[4], score[4]) per tile, then fq(quad) per quad.
-  auto replay = [&](auto&& f, auto&& fq) {
-    for (int c = wave; kRun * c < nquad; c += kGroupWaves) {
-      floatx4 qv[kRun][4];
-#pragma unroll
-      for (int r = 0; r < kRun; ++r) load_quad(kRun * c + r, qv[r]);
-#pragma unroll
-      for (int r = 0; r < kRun; ++r) {
-        const int j = kRun * c + r;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int col = (4 * j + u) * 16 + lr;
-          bool valid[4];
-          slot_valid(col, valid);
-          const float sc[4] = {qv[r][u][0], qv[r][u][1], qv[r][u][2], qv[r][u][3]};
-          f(j, u, col, valid, sc);
-        }
-        fq(j);
-      }
-    }
-  };
 
   if constexpr (kPhase == 1) {
     // ---- row variance (population, over the row's causal scores) --------------
-    // Sums of d = s - c and d^2 with c = the row's mean estimated from its
-    // histogram (bin centres; |mean - c| <= half a bin), so that the
-    // difference S2/n - (S1/n)^2 keeps its precision.  Then the histograms
-    // are saved for phase 2.
-    __shared__ float st_shift[16];
+    // Sums of d = s - c and d^2 with c = the sample's mean from its histogram's
+    // bin centres (|mean - c| is about a bin width), so that S2/n - (S1/n)^2
+    // keeps its precision.  Then the histograms are saved for phase 2.
+    __shared__ float st_c[16];
     __shared__ float2 st_part[16 * kGroupWaves];
-    if (wave == 0 && lr == 0) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) st_shift[4 * g + e] = inv_w[e];   // 1 / bin width
-    }
-    __syncthreads();
-    {
-      const int rl = (tid >> 4) & 15, part = tid & 15;   // threads 0..255: 16 per row, 32 bins each
-      float m = 0.f;
-      if (tid < 256)
-        for (int bin = part * (kNB / 16); bin < (part + 1) * (kNB / 16); ++bin)
-          m = __builtin_fmaf((float)H::count(&sh[rl * kHStride], bin), (float)bin + 0.5f, m);
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) m += __shfl_xor(m, o, 64);
-      const int row = r0 + rl;
-      const float iw = st_shift[rl];
-      __syncthreads();
-      if (tid < 256 && part == 0) st_shift[rl] = row < p.T ? m / ((float)(row + 1) * iw) : 0.f;
-    }
-    __syncthreads();
-    float c[4], s1[4], s2[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      c[e] = st_shift[4 * g + e];
-      s1[e] = 0.f;
-      s2[e] = 0.f;
-    }
-    replay(
-        [&](int, int, int, const bool (&valid)[4], const float (&sc)[4]) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float d = valid[e] ? sc[e] - c[e] : 0.f;
-            s1[e] += d;
-            s2[e] = __builtin_fmaf(d, d, s2[e]);
-          }
-        },
-        [](int) {});
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
+    if (tid < 256) {
+      const int rl = tid >> 4, part = tid & 15;   // 16 threads per row, 64 bins each
+      float m = 0.f, n = 0.f;
+      for (int bin = part * (kNB / 16); bin < (part + 1) * (kNB / 16); ++bin) {
+        const float c = (float)hist_count(&pool[rl * kHStride], bin);
+        m = __builtin_fmaf(c, (float)bin + 0.5f, m);
+        n += c;
+      }
 #pragma unroll
       for (int o = 1; o < 16; o <<= 1) {
-        s1[e] += __shfl_xor(s1[e], o, 64);
-        s2[e] += __shfl_xor(s2[e], o, 64);
+        m += __shfl_xor(m, o, 64);
+        n += __shfl_xor(n, o, 64);
       }
-    if (lr == 0) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) st_part[(4 * g + e) * kGroupWaves + wave] = make_float2(s1[e], s2[e]);
+      if (part == 0) st_c[rl] = n > 0.f ? m / (n * st_invw[rl]) : 0.f;
     }
+    __syncthreads();
+    const float c = st_c[lr];
+    float s1 = 0.f, s2 = 0.f;
+    sweep(wave, round_robin, [&](int t, const float (&sc)[4]) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = (act && 16 * t + 4 * g + e <= row) ? sc[e] - c : 0.f;
+        s1 += d;
+        s2 = __builtin_fmaf(d, d, s2);
+      }
+    });
+    s1 += __shfl_xor(s1, 16, 64);
+    s2 += __shfl_xor(s2, 16, 64);
+    s1 += __shfl_xor(s1, 32, 64);
+    s2 += __shfl_xor(s2, 32, 64);
+    if (g == 0) st_part[lr * kGroupWaves + wave] = make_float2(s1, s2);
     __syncthreads();
     if (tid < 16 && r0 + tid < p.T) {
       float S1 = 0.f, S2 = 0.f;
@@ -514,209 +521,335 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_bits_kernel(IdxArgs p, 
       sa.row_var[(int64_t)b * p.T + r0 + tid] = fmaxf(S2 / n - m1 * m1, 0.f);
     }
     uint32_t* hdst = sa.hist + (int64_t)blockIdx.x * (16 * kHStride);
-    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) hdst[i] = sh[i];
+    for (int i = tid; i < 16 * kHStride; i += kGroupThreads) hdst[i] = pool[i];
     return;
   }
 
-  // ---- pass 2: bins above b1 -> mask words; bin b1 -> candidates -------------
-  // Candidates of row 4g+e found by this wave go to its own region of the
-  // row's list in the workspace (kWCap slots), positions from a per-wave
-  // count: no atomics.  Lane
-  // 16g+e assembles row 4g+e's 64-bit mask word of each quad.
-  int wc[4] = {0, 0, 0, 0};
-  const uint32_t below = (1u << lr) - 1u;
-  uint64_t word = 0;
-  replay(
-      [&](int, int u, int col, const bool (&valid)[4], const float (&sc)[4]) {
-        uint64_t m[4];
+  // ---- band: wave w takes row w ------------------------------------------------
+  {
+    const int rl = wave;
+    if (st_mode[rl] == kActive) {
+      const uint32_t* hr = pool + rl * kHStride;
+      int cnt[16];
+      int v = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int bn = bin_of(sc[e], inv_w[e]);
-          m[e] = ballot64(valid[e] && bn > b1[e]);
-          const bool is_cand = valid[e] && bn == b1[e];
-          const uint64_t cm = ballot64(is_cand);
-          if (cm) {
-            const uint32_t gm = (uint32_t)(cm >> (16 * g)) & 0xffffu;
-            const int pos = wc[e] + __popc(gm & below);
-            if (is_cand && pos < kWCap)
-              cand[(4 * g + e) * kCap + wave * kWCap + pos] = uint2{score_key(sc[e]), (uint32_t)col};
-            wc[e] += __popc(gm);
+      for (int i = 0; i < 16; ++i) {
+        cnt[i] = hist_count(hr, 16 * lane + i);
+        v += cnt[i];
+      }
+      const int suf = wave_suffix(v, lane);          // samples in bins >= 16 * lane
+      const int n_s = __shfl(suf, 0, 64);
+      const float n = (float)(r0 + rl + 1), kf = (float)st_k[rl];
+      const float pk = kf / n;
+      const float rstar = kf * (float)n_s / n;
+      const float var = (float)n_s * pk * (1.f - pk) * (1.f - (float)n_s / n);
+      const float delta = kBandZ * __builtin_sqrtf(fmaxf(var, 0.f)) + 2.f;
+      const float r_hi = rstar - delta, r_lo = rstar + delta;
+      // C(b) = samples in bins >= b.  hi: the lowest bin with C(b) <= r_hi;
+      // lo: the highest bin with C(b) >= r_lo.
+      int bhi = kNB, blo = -1, c = suf;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int bin = 16 * lane + i;
+        if ((float)c <= r_hi) bhi = min(bhi, bin);
+        if ((float)c >= r_lo) blo = bin;
+        c -= cnt[i];
+      }
+      bhi = wave_min(bhi);
+      blo = wave_max(blo);
+      if (lane == 0) {
+        const float iw = st_invw[rl];
+        st_hi[rl] = bhi >= kNB ? __builtin_inff() : (float)bhi / iw;
+        st_lo[rl] = blo <= 0 ? -__builtin_inff() : (float)blo / iw;
+      }
+    }
+  }
+  __syncthreads();   // the histograms are dead from here: the pool holds the candidate lists
+
+  // ---- main pass: sure winners -> mask words, band -> candidate lists ---------
+  {
+    const float lo = act ? st_lo[lr] : __builtin_inff();
+    const float hi = act ? st_hi[lr] : __builtin_inff();
+    uint2* wdst = (g == 0 && act) ? reinterpret_cast<uint2*>(bbase + (int64_t)row * b_st) : nullptr;
+    uint32_t* mykey = ckey + lr * kRowCap;
+    uint16_t* mypos = cpos + lr * kRowCap;
+    int nsure = 0;
+    // One tile's scores -> sure bits in w2, candidates appended to the row's list.
+    auto classify = [&](int t, int u, const float (&sc)[4], uint32_t (&w2)[2]) {
+      const bool diag = t == ntl - 1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float s = sc[e];
+        const bool valid = act && (!diag || 4 * g + e <= lr);
+        const bool le = s <= hi;
+        const bool sure = valid && !le;               // NaN ranks above every number
+        const bool cand = valid && le && s >= lo;
+        w2[u >> 1] |= sure ? (1u << (16 * (u & 1) + 4 * g + e)) : 0u;
+        if (cand) {
+          const uint32_t at = atomicAdd(&st_cnt[lr], 1u);
+          if (at < (uint32_t)kRowCap) {
+            mykey[at] = score_key(s);
+            mypos[at] = (uint16_t)(16 * t + 4 * g + e);
           }
         }
-        const uint64_t me = (lr & 2) ? ((lr & 1) ? m[3] : m[2]) : ((lr & 1) ? m[1] : m[0]);
-        word |= ((me >> (16 * g)) & 0xffffull) << (16 * u);
-      },
-      [&](int j) {
-        if (own_act && j < nquad) reinterpret_cast<uint64_t*>(bbase + (int64_t)own_row * b_st)[j] = word;
-        word = 0;
-      });
-  if (lr == 0) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sh_wcnt[(4 * g + e) * kGroupWaves + wave] = (uint32_t)wc[e];
+      }
+    };
+    auto put_word = [&](int qd, const uint32_t (&w2)[2]) {
+      const uint32_t lo32 = or_row4(w2[0]), hi32 = or_row4(w2[1]);
+      uint2* dst = wdst ? wdst + qd : scratch;
+      *dst = uint2{lo32, hi32};
+      nsure += __popc(lo32) + __popc(hi32);
+    };
+    // Complete quads of this wave (wave, wave + 16, ...): even tiles of a quad
+    // use key buffer A, odd ones B.  Every turn issues the same memory
+    // operations -- four key-tile loads and one word store -- and the loop is
+    // entered after one load and one (scratch) store, so the compiler's wait
+    // for a buffer always leaves the other buffer's load in flight.
+    const int nfull = ntl >> 2;
+    Op kA[kS], kB[kS];
+    rgp.load_keys(16 * min(4 * wave, ntl - 1), p.T, lane, kA);
+    *scratch = uint2{0u, 0u};
+    for (int qd = wave; qd < nfull; qd += kGroupWaves) {
+      uint32_t w2[2] = {0u, 0u};
+      const int t0 = 4 * qd;
+      float sc[4];
+      rgp.load_keys(16 * (t0 + 1), p.T, lane, kB);
+      tile(kA, sc);
+      classify(t0, 0, sc, w2);
+      rgp.load_keys(16 * (t0 + 2), p.T, lane, kA);
+      tile(kB, sc);
+      classify(t0 + 1, 1, sc, w2);
+      rgp.load_keys(16 * (t0 + 3), p.T, lane, kB);
+      tile(kA, sc);
+      classify(t0 + 2, 2, sc, w2);
+      rgp.load_keys(16 * min(t0 + 4 * kGroupWaves, ntl - 1), p.T, lane, kA);
+      tile(kB, sc);
+      classify(t0 + 3, 3, sc, w2);
+      put_word(qd, w2);
+    }
+    // The last, partial quad (1-3 tiles) belongs to wave nfull % 16.
+    if ((ntl & 3) && wave == nfull % kGroupWaves) {
+      uint32_t w2[2] = {0u, 0u};
+      for (int u = 0; u < (ntl & 3); ++u) {
+        const int t = 4 * nfull + u;
+        Op kb[kS];
+        rgp.load_keys(16 * t, p.T, lane, kb);
+        float sc[4];
+        tile(kb, sc);
+        classify(t, u, sc, w2);
+      }
+      put_word(nfull, w2);
+    }
+    if (g == 0) st_sure[lr * kGroupWaves + wave] = act ? nsure : 0;
   }
-  // The resolve's atomics and candidate reads below come from waves of this
-  // block only: the barrier (a workgroup-scope release/acquire) orders the
-  // mask and candidate stores above before them.  A device-scope fence here
-  // would write back the whole L2.
+  // The resolve ORs winners into the words stored above, by atomics that
+  // execute in L2, from other waves.  A workgroup-scope barrier does not wait
+  // for this wave's stores to reach L2 (they are visible to the workgroup
+  // through the CU's cache first), so a late store could overwrite the ORed
+  // bits: wait for them explicitly before the barrier.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
 
-  // ---- resolve: wave w takes rows kRW*w .. kRW*w + kRW-1 ----------------------
-  // Candidate slot i*64 + lane lies in region i/2 at position (i%2)*64 + lane.
-  constexpr int kRW = 16 / kGroupWaves;
-  for (int q = 0; q < kRW; ++q) {
-    const int rl = kRW * wave + q;
-    if (st_mode[rl] != kActive) continue;
-    int nw[kGroupWaves];
-    bool ovf = false;
+  // ---- resolve: wave w takes row w -----------------------------------------------
+  {
+    const int rl = wave;
+    if (st_mode[rl] == kActive) {
+      int n_sure = 0;
 #pragma unroll
-    for (int w = 0; w < kGroupWaves; ++w) {
-      nw[w] = (int)sh_wcnt[rl * kGroupWaves + w];
-      ovf |= nw[w] > kWCap;
-    }
-    if (ovf) {
-      if (lane == 0) { st_mode[rl] = kOverflow; st_any[1] = 1; }
-      continue;
-    }
-    // The row's n candidates, compacted: candidate j (in the regions' order)
-    // goes to slot j / 64, lane j % 64, so the radix passes below ballot
-    // ceil(n / 64) slots instead of one per occupied region half.
-    constexpr int kSlots = kCap / 64;
-    int start[kGroupWaves];
-    int n = 0;
+      for (int w = 0; w < kGroupWaves; ++w) n_sure += st_sure[rl * kGroupWaves + w];
+      const int n_all = (int)st_cnt[rl];
+      int need = st_k[rl] - n_sure;
+      if (sa.force_fallback || n_all > kRowCap || need < 0 || n_all < need) {
+        if (lane == 0) { st_mode[rl] = kFailed; st_any[1] = 1; }
+      } else if (need > 0) {
+        const uint32_t* lk = ckey + rl * kRowCap;
+        const uint16_t* lp = cpos + rl * kRowCap;
+        const int n = n_all;
+        // theta = the need-th largest candidate key, MSB-first over the bits on
+        // which the candidates differ, 8-bit digits counted in LDS.
+        uint32_t kor = 0u, kand = ~0u;
+        for (int i = lane; i < n; i += 64) { kor |= lk[i]; kand &= lk[i]; }
 #pragma unroll
-    for (int w = 0; w < kGroupWaves; ++w) { start[w] = n; n += nw[w]; }
-    uint32_t cv[kSlots], ci[kSlots];
-    bool cvalid[kSlots], used[kSlots];
-    uint32_t kor = 0u, kand = ~0u;
+        for (int o = 1; o < 64; o <<= 1) {
+          kor |= (uint32_t)__shfl_xor((int)kor, o, 64);
+          kand &= (uint32_t)__shfl_xor((int)kand, o, 64);
+        }
+        const uint32_t diff = kor ^ kand;
+        int rem = diff ? 32 - __builtin_clz(diff) : 0;       // low bits still open
+        uint32_t prefix = rem >= 32 ? 0u : (kand & (~0u << rem));
+        uint32_t* rh = sh_rh[wave];
+        while (rem > 0) {
+          const int nb = rem < 8 ? rem : 8, shift = rem - nb;
+          const uint32_t hmask = rem >= 32 ? 0u : ~0u << rem;
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const int j = i * 64 + lane;
-      used[i] = i * 64 < n;
-      cvalid[i] = j < n;
-      int w = 0;
+          for (int i = 0; i < 4; ++i) rh[4 * lane + i] = 0u;
+          wave_lds_sync();
+          for (int i = lane; i < n; i += 64) {
+            const uint32_t kk = lk[i];
+            if ((kk & hmask) == prefix) atomicAdd(&rh[(kk >> shift) & ((1u << nb) - 1u)], 1u);
+          }
+          wave_lds_sync();
+          int cb[4], vsum = 0;
 #pragma unroll
-      for (int ww = 1; ww < kGroupWaves; ++ww) w += j >= start[ww] ? 1 : 0;
-      const uint2 cd = cvalid[i] ? cand[rl * kCap + w * kWCap + (j - start[w])] : uint2{0u, 0u};
-      cv[i] = cd.x;
-      ci[i] = cd.y;
-      if (cvalid[i]) { kor |= cv[i]; kand &= cv[i]; }
-    }
-    // Bits on which every candidate agrees are part of theta; the radix
-    // select starts at the highest bit on which they differ.
+          for (int i = 0; i < 4; ++i) { cb[i] = (int)rh[4 * lane + i]; vsum += cb[i]; }
+          const int suf = wave_suffix(vsum, lane);            // keys in digits >= 4 * lane
+          // the highest digit d with count(digits >= d) >= need
+          int dsel = -1, above = 0, c = suf;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      kor |= (uint32_t)__shfl_xor((int)kor, o, 64);
-      kand &= (uint32_t)__shfl_xor((int)kand, o, 64);
-    }
-    int k = st_need[rl];
-    const uint32_t diff = kor ^ kand;
-    const int top = diff ? 31 - __builtin_clz(diff) : -1;
-    uint32_t pmask = top >= 31 ? 0u : ~0u << (top + 1);
-    uint32_t prefix = kand & pmask;
-    for (int bit = top; bit >= 0; --bit) {
-      const uint32_t tm = pmask | (1u << bit), tv = prefix | (1u << bit);
-      int c = 0;
+          for (int i = 0; i < 4; ++i) {
+            if (c >= need) { dsel = 4 * lane + i; above = c - cb[i]; }
+            c -= cb[i];
+          }
+          const int d = wave_max(dsel);
+          need -= __shfl(above, d >> 2, 64);
+          prefix |= (uint32_t)d << shift;
+          rem = shift;
+        }
+        const uint32_t theta = prefix;
+        int ties = 0;
+        for (int i = lane; i < n; i += 64) ties += lk[i] == theta ? 1 : 0;
 #pragma unroll
-      for (int i = 0; i < kSlots; ++i)
-        if (used[i]) c += __popcll(ballot64(cvalid[i] && (cv[i] & tm) == tv));
-      if (c >= k) prefix = tv; else k -= c;
-      pmask = tm;
-    }
-    // winners: key > theta, or key == theta among the k lowest indices of the
-    // ties (all of them when there are at most k)
-    int ties = 0;
+        for (int o = 1; o < 64; o <<= 1) ties += __shfl_xor(ties, o, 64);
+        uint32_t istar = 0xffffffffu;
+        if (ties > need) {       // rare: the need lowest indices among the ties, 9-bit digits
+          uint32_t ip = 0u;
+          for (int lvl = 0; lvl < 2; ++lvl) {
+            const int shift = 9 * (1 - lvl);
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i)
-      if (used[i]) ties += __popcll(ballot64(cvalid[i] && cv[i] == prefix));
-    const int row = r0 + rl;
-    uint32_t* brow = bbase + (int64_t)row * b_st;
-#pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      if (!used[i] || !cvalid[i]) continue;
-      bool win = cv[i] > prefix;
-      if (cv[i] == prefix) {
-        if (ties <= k) {
-          win = true;
-        } else {
-          int rank = 0;
-          for (int w = 0; w < kGroupWaves; ++w)
-            for (int o = 0; o < nw[w]; ++o) {
-              const uint2 cd = cand[rl * kCap + w * kWCap + o];
-              rank += (cd.x == prefix && cd.y < ci[i]) ? 1 : 0;
+            for (int i = 0; i < 4; ++i) rh[4 * lane + i] = 0u;   // 512 digits as 16-bit counts
+            wave_lds_sync();
+            for (int i = lane; i < n; i += 64) {
+              if (lk[i] != theta) continue;
+              const int ix = lp[i];
+              if (lvl == 0 || ((uint32_t)ix >> 9) == ip) {
+                const int dg = (ix >> shift) & 511;
+                atomicAdd(&rh[dg >> 1], 1u << (16 * (dg & 1)));
+              }
             }
-          win = rank < k;
+            wave_lds_sync();
+            int cb[8], vsum = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const int dg = 8 * lane + i;
+              cb[i] = (int)((rh[dg >> 1] >> (16 * (dg & 1))) & 0xffffu);
+              vsum += cb[i];
+            }
+            // the lowest digit d with count(digits <= d) >= need
+            int dsel = 512, below = 0, c = wave_prefix(vsum, lane) - vsum;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              if (c + cb[i] >= need && dsel == 512) { dsel = 8 * lane + i; below = c; }
+              c += cb[i];
+            }
+            const int d = wave_min(dsel);
+            need -= __shfl(below, d >> 3, 64);
+            ip = (ip << 9) | (uint32_t)d;
+          }
+          istar = ip;
+        }
+        uint32_t* brow = bbase + (int64_t)(r0 + rl) * b_st;
+        for (int i = lane; i < n; i += 64) {
+          const uint32_t kk = lk[i];
+          const int ix = lp[i];
+          if (kk > theta || (kk == theta && (uint32_t)ix <= istar)) atomicOr(&brow[ix >> 5], 1u << (ix & 31));
         }
       }
-      if (win) atomicOr(&brow[ci[i] >> 5], 1u << (ci[i] & 31));
     }
   }
   __syncthreads();
   if (!st_any[1]) return;
 
-  // ---- overflow rows: radix passes over the stored scores of bin b1 -----------
-  if (tid < 16 && st_mode[tid] == kOverflow) st_key[tid] = 0u;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) act[e] = st_mode[4 * g + e] == kOverflow;
+  // ---- fallback: exact radix select over recomputed scores of failed rows ------
+  const bool fb = st_mode[lr] == kFailed;
+  if (tid < 16) {
+    st_need[tid] = st_k[tid];
+    st_key[tid] = 0u;
+    st_idx[tid] = 0u;
+  }
   for (int level = 0; level < 4; ++level) {
-    uint32_t pre[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) pre[e] = st_key[4 * g + e];
-    const int hi_shift = 32 - 8 * level, lo_shift = 24 - 8 * level;
-    zero_hist();
-    replay(
-        [&](int, int, int, const bool (&valid)[4], const float (&sc)[4]) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (valid[e] && bin_of(sc[e], inv_w[e]) == b1[e]) {
-              const uint32_t key = score_key(sc[e]);
-              if (level == 0 || (key >> hi_shift) == pre[e])
-                atomicAdd(&sh[(4 * g + e) * kHStride + ((key >> lo_shift) & 255u)], 1u);
-            }
-          }
-        },
-        [](int) {});
+    for (int i = tid; i < 16 * kFbStride; i += kGroupThreads) pool[i] = 0u;
     __syncthreads();
-    if (tid < 16 && st_mode[tid] == kOverflow) {
+    const uint32_t pre = st_key[lr];
+    const int ls = 24 - 8 * level;
+    sweep(wave, round_robin, [&](int t, const float (&sc)[4]) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (fb && 16 * t + 4 * g + e <= row) {
+          const uint32_t kk = score_key(sc[e]);
+          if (level == 0 || (kk >> (ls + 8)) == pre) atomicAdd(&pool[lr * kFbStride + ((kk >> ls) & 255u)], 1u);
+        }
+      }
+    });
+    __syncthreads();
+    if (tid < 16 && st_mode[tid] == kFailed) {
       int cum = 0, d = 0, nd = st_need[tid];
       for (int bin = 255; bin >= 0; --bin) {
-        const int c = (int)sh[tid * kHStride + bin];
-        if (cum + c >= nd) { d = bin; break; }
+        const int c = (int)pool[tid * kFbStride + bin];
+        if (cum + c >= nd) { d = bin; st_ties[tid] = c; break; }
         cum += c;
       }
       st_need[tid] = nd - cum;
       st_key[tid] = (st_key[tid] << 8) | (uint32_t)d;
+      if (level == 3 && st_ties[tid] > st_need[tid]) st_any[2] = 1;
     }
     __syncthreads();
   }
-  // wave 0 marks the winners of the overflow rows in key order (tie ranks need
-  // order); every wave's stored tiles are visible after the barriers above
-  if (wave == 0) {
-    uint32_t theta[4];
-    int tie_need[4], tie_seen[4];
+  // ties at the threshold beyond the need: the need lowest indices (< 2^16)
+  const bool ix_row = fb && st_ties[lr] > st_need[lr];
+  if (st_any[2]) {
+    for (int lvl = 0; lvl < 2; ++lvl) {
+      for (int i = tid; i < 16 * kFbStride; i += kGroupThreads) pool[i] = 0u;
+      __syncthreads();
+      const uint32_t theta = st_key[lr], ip = st_idx[lr];
+      const int shift = 9 * (1 - lvl);
+      sweep(wave, round_robin, [&](int t, const float (&sc)[4]) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      theta[e] = st_key[4 * g + e];
-      tie_need[e] = st_need[4 * g + e];
-      tie_seen[e] = 0;
-    }
-    const uint64_t gmask = 0xffffull << (16 * g);
-    for (int t = 0; t < ntl; ++t) {
-      const floatx4 v = *reinterpret_cast<const floatx4*>(wsg + t * kTile + lane * 4);
-      const int col = t * 16 + lr;
-      bool valid[4];
-      slot_valid(col, valid);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = r0 + 4 * g + e;
-        const bool inbin = valid[e] && bin_of(v[e], inv_w[e]) == b1[e];
-        const uint32_t key = score_key(v[e]);
-        const bool tie = inbin && key == theta[e];
-        const uint64_t tmask = ballot64(tie) & gmask;
-        const int trank = tie_seen[e] + count_below(tmask);
-        tie_seen[e] += __popcll(tmask);
-        if (inbin && (key > theta[e] || (tie && trank < tie_need[e])))
-          atomicOr(&bbase[(int64_t)row * b_st + (col >> 5)], 1u << (col & 31));
+        for (int e = 0; e < 4; ++e) {
+          const int col = 16 * t + 4 * g + e;
+          if (ix_row && col <= row && score_key(sc[e]) == theta && (lvl == 0 || ((uint32_t)col >> 9) == ip))
+            atomicAdd(&pool[lr * kFbStride + ((col >> shift) & 511)], 1u);
+        }
+      });
+      __syncthreads();
+      if (tid < 16 && st_mode[tid] == kFailed && st_ties[tid] > st_need[tid]) {
+        int cum = 0, d = 0;
+        const int nd = st_need[tid];
+        for (int bin = 0; bin < 512; ++bin) {
+          const int c = (int)pool[tid * kFbStride + bin];
+          if (cum + c >= nd) { d = bin; break; }
+          cum += c;
+        }
+        st_idx[tid] = (st_idx[tid] << 9) | (uint32_t)d;
+        if (lvl == 0) st_need[tid] = nd - cum;      // the first digit's lower ties are all taken
       }
+      __syncthreads();
+    }
+  }
+  // marking: every word of a failed row is rewritten
+  {
+    const uint32_t theta = st_key[lr];
+    const uint32_t istar = ix_row ? st_idx[lr] : 0xffffffffu;
+    uint2* wdst = (g == 0 && fb) ? reinterpret_cast<uint2*>(bbase + (int64_t)row * b_st) : nullptr;
+    for (int qd = wave; 4 * qd < ntl; qd += kGroupWaves) {
+      uint32_t w2[2] = {0u, 0u};
+      for (int u = 0; u < 4; ++u) {
+        const int t = 4 * qd + u;
+        if (t >= ntl) break;
+        Op kb[kS];
+        rgp.load_keys(16 * t, p.T, lane, kb);
+        floatx4 acc[kHi];
+        rgp.mma(kb, acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int col = 16 * t + 4 * g + e;
+          const uint32_t kk = score_key(rgp.score(acc, e));
+          const bool sel = fb && col <= row && (kk > theta || (kk == theta && (uint32_t)col <= istar));
+          w2[u >> 1] |= sel ? (1u << (16 * (u & 1) + 4 * g + e)) : 0u;
+        }
+      }
+      const uint32_t lo32 = or_row4(w2[0]), hi32 = or_row4(w2[1]);
+      uint2* dst = wdst ? wdst + qd : scratch;
+      *dst = uint2{lo32, hi32};
     }
   }
 }
@@ -812,7 +945,13 @@ __global__ __launch_bounds__(1024) void adaptive_k_kernel(const float* __restric
 // ---------------------------------------------------------------------------
 // Host entry points
 // ---------------------------------------------------------------------------
+#include <atomic>
+
 using namespace gsa_host;
+
+// Process-wide test hook: every active row of the fused selector takes the
+// exact fallback path (gsa_debug_force_select_fallback).
+static std::atomic<int> g_force_fallback{0};
 
 static int check_indexer_args(const void* q, int64_t q_sb, int64_t q_st, const void* k, int64_t k_sb,
                               int64_t k_st, const void* w, const float* bias, int B, int T, int Hi,
@@ -852,46 +991,64 @@ extern "C" int gsa_indexer_scores(const void* q_idx, int64_t q_sb, int64_t q_st,
   gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
   const int ngroups = (T + 15) / 16;
   const int waves = B * ngroups;
+  const int vec = aligned(scores, 16) && (s_st % 4) == 0 && (s_sb % 4) == 0;
   dim3 grid((waves + 3) / 4), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == GSA_DTYPE_BF16)
-    hipLaunchKernelGGL(gsa::indexer_scores_kernel<uint16_t>, grid, block, 0, s, a, causal, scores, s_sb, s_st);
+    hipLaunchKernelGGL(gsa::indexer_scores_kernel<uint16_t>, grid, block, 0, s, a, causal, scores, s_sb, s_st, vec);
   else
-    hipLaunchKernelGGL(gsa::indexer_scores_kernel<float>, grid, block, 0, s, a, causal, scores, s_sb, s_st);
+    hipLaunchKernelGGL(gsa::indexer_scores_kernel<float>, grid, block, 0, s, a, causal, scores, s_sb, s_st, vec);
   return launch_status();
 }
 
-// One launch of the fused selector in phase kPhase; the 16-bit histogram
-// counts are exact while a row has at most 65535 keys.
-template <int kPhase>
-static void launch_bits(const gsa::IdxArgs& a, const gsa::SelArgs& sa, int dtype, uint32_t* bits,
-                        int64_t b_sb, int64_t b_st, float* wsf, uint2* wsc, hipStream_t s) {
-  const bool packed = a.T <= 65535;
-  const dim3 grid(a.B * ((a.T + 15) / 16)), block(gsa::kGroupThreads);
-  if (dtype == GSA_DTYPE_BF16) {
-    if (packed)
-      hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, true, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);
-    else
-      hipLaunchKernelGGL((gsa::indexer_bits_kernel<uint16_t, false, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);
-  } else {
-    if (packed)
-      hipLaunchKernelGGL((gsa::indexer_bits_kernel<float, true, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);
-    else
-      hipLaunchKernelGGL((gsa::indexer_bits_kernel<float, false, kPhase>), grid, block, 0, s, a, sa, bits, b_sb, b_st, wsf, wsc);
+// The selector's blocks use more LDS than the 64 KiB default: raise each
+// instantiation's limit once per device.  (A benign race: concurrent first
+// calls both set the same attribute.)
+static constexpr int kMaxDevices = 64;
+
+template <typename Kern>
+static int raise_lds_limit(Kern kern, bool (&done)[kMaxDevices]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return GSA_ERR_SHAPE;
+  if (!done[dev]) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsa::kPoolBytes);
+    if (e != hipSuccess) return -static_cast<int>(e);
+    done[dev] = true;
   }
+  return GSA_OK;
 }
 
-// Score tiles (1 KiB per causal 16x16 tile), then the candidate lists
-// (16 rows x kCap (key, index) pairs per 16-row group).
-static size_t score_ws_bytes(int B, int T) {
-  const size_t g = (size_t)((T + 15) / 16);
-  return (size_t)B * (g * (g + 1) / 2) * gsa::kTile * sizeof(float);
+// One launch of the fused selector in phase kPhase.
+template <typename T, int kPhase>
+static int launch_select_t(const gsa::IdxArgs& a, const gsa::SelArgs& sa, uint32_t* bits, int64_t b_sb,
+                           int64_t b_st, uint8_t* ws, hipStream_t s) {
+  static bool lds_set[kMaxDevices] = {};
+  const int st = raise_lds_limit(gsa::indexer_select_kernel<T, kPhase>, lds_set);
+  if (st) return st;
+  const dim3 grid(a.B * ((a.T + 15) / 16)), block(gsa::kGroupThreads);
+  hipLaunchKernelGGL((gsa::indexer_select_kernel<T, kPhase>), grid, block, gsa::kPoolBytes, s, a, sa, bits, b_sb,
+                     b_st, ws);
+  return launch_status();
 }
 
+template <int kPhase>
+static int launch_select(const gsa::IdxArgs& a, gsa::SelArgs sa, int dtype, uint32_t* bits, int64_t b_sb,
+                         int64_t b_st, uint8_t* ws, hipStream_t s) {
+  sa.force_fallback = g_force_fallback.load(std::memory_order_relaxed);
+  if (dtype == GSA_DTYPE_BF16) return launch_select_t<uint16_t, kPhase>(a, sa, bits, b_sb, b_st, ws, s);
+  return launch_select_t<float, kPhase>(a, sa, bits, b_sb, b_st, ws, s);
+}
+
+// The candidate lists live in LDS: the workspace holds only the store slots of
+// lanes without a mask word to write (kScratchBytes per 16-row group).
 extern "C" size_t gsa_indexer_select_workspace_bytes(int B, int T) {
   if (B < 1 || T < 1) return 0;
-  const size_t g = (size_t)((T + 15) / 16);
-  return score_ws_bytes(B, T) + (size_t)B * g * 16 * gsa::kCap * sizeof(uint2);
+  return (size_t)B * (size_t)((T + 15) / 16) * gsa::kScratchBytes;
+}
+
+extern "C" int gsa_debug_force_select_fallback(int on) {
+  return g_force_fallback.exchange(on ? 1 : 0);
 }
 
 int gsa_host::launch_adaptive_k(const float* var, int n, int k_base, int k_min, int k_max, int k_cap,
@@ -910,6 +1067,7 @@ static int check_select_args(const void* q_idx, int64_t q_sb, int64_t q_st, cons
   if (st) return st;
   if (!bits || !ws) return GSA_ERR_NULL;
   if ((idx_out == nullptr) != (count_out == nullptr)) return GSA_ERR_NULL;
+  if (T > gsa::kMaxSelectT) return GSA_ERR_SHAPE;
   const int W = 2 * ((T + 63) / 64);
   if (b_st < W || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
   if (!aligned(bits, 8) || (b_st % 2) || (b_sb % 2)) return GSA_ERR_ALIGN;
@@ -934,11 +1092,8 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
   if (ws_bytes < gsa_indexer_select_workspace_bytes(B, T)) return GSA_ERR_SHAPE;
   gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  float* wsf = static_cast<float*>(ws);
-  uint2* wsc = reinterpret_cast<uint2*>(static_cast<char*>(ws) + score_ws_bytes(B, T));
-  gsa::SelArgs sa{k_eff, nullptr, nullptr, nullptr};
-  launch_bits<0>(a, sa, dtype, bits, b_sb, b_st, wsf, wsc, s);
-  st = launch_status();
+  st = launch_select<0>(a, gsa::SelArgs{k_eff, nullptr, nullptr, nullptr, 0}, dtype, bits, b_sb, b_st,
+                        static_cast<uint8_t*>(ws), s);
   if (st || !idx_out) return st;
   const int W = 2 * ((T + 63) / 64);
   hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_eff,
@@ -946,15 +1101,14 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
   return launch_status();
 }
 
-// Adaptive workspace: the fixed selector's, then the phase-1 histograms (16
-// rows x Hist::kStride words per 16-row group), then the per-row variances
-// and k values ([B*T] each, used when the caller does not take them).
+// Adaptive workspace: the fixed selector's, then the sample histograms kept
+// between the launches (16 rows x kHStride words per 16-row group), then the
+// per-row variances and k values ([B*T] each, used when the caller does not
+// take them).
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 static size_t hist_ws_bytes(int B, int T) {
-  const size_t g = (size_t)((T + 15) / 16);
-  const size_t stride = T <= 65535 ? gsa::Hist<true>::kStride : gsa::Hist<false>::kStride;
-  return (size_t)B * g * 16 * stride * sizeof(uint32_t);
+  return (size_t)B * (size_t)((T + 15) / 16) * 16 * gsa::kHStride * sizeof(uint32_t);
 }
 
 extern "C" size_t gsa_indexer_select_adaptive_workspace_bytes(int B, int T) {
@@ -982,9 +1136,7 @@ extern "C" int gsa_indexer_select_adaptive(const void* q_idx, int64_t q_sb, int6
   const int k_cap = k_max < T ? k_max : T;
   gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  char* base = static_cast<char*>(ws);
-  float* wsf = reinterpret_cast<float*>(base);
-  uint2* wsc = reinterpret_cast<uint2*>(base + score_ws_bytes(B, T));
+  uint8_t* base = static_cast<uint8_t*>(ws);
   size_t off = align256(gsa_indexer_select_workspace_bytes(B, T));
   uint32_t* hist = reinterpret_cast<uint32_t*>(base + off);
   off += align256(hist_ws_bytes(B, T));
@@ -992,11 +1144,10 @@ extern "C" int gsa_indexer_select_adaptive(const void* q_idx, int64_t q_sb, int6
   off += align256((size_t)B * T * sizeof(float));
   int32_t* krow = k_out ? k_out : reinterpret_cast<int32_t*>(base + off);
 
-  launch_bits<1>(a, gsa::SelArgs{0, nullptr, var, hist}, dtype, bits, b_sb, b_st, wsf, wsc, s);
-  if ((st = launch_status())) return st;
+  if ((st = launch_select<1>(a, gsa::SelArgs{0, nullptr, var, hist, 0}, dtype, bits, b_sb, b_st, base, s)))
+    return st;
   if ((st = launch_adaptive_k(var, B * T, k_base, k_min, k_max, k_cap, krow, s))) return st;
-  launch_bits<2>(a, gsa::SelArgs{0, krow, nullptr, hist}, dtype, bits, b_sb, b_st, wsf, wsc, s);
-  st = launch_status();
+  st = launch_select<2>(a, gsa::SelArgs{0, krow, nullptr, hist, 0}, dtype, bits, b_sb, b_st, base, s);
   if (st || !idx_out) return st;
   const int W = 2 * ((T + 63) / 64);
   hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_cap,

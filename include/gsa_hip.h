@@ -129,12 +129,15 @@ int gsa_topk_select_adaptive(const float* scores, int64_t s_sb, int64_t s_st,
  * takes.  When idx_out and count_out are given it also writes, like
  * GSA_ORDER_INDEX_ASC: idx_out int32 [B,T,k_eff] = row t's min(t+1, k_eff)
  * selected keys ascending, followed by t+1, t+2, ...; count_out int32 [B,T].
- * ws: caller-provided device workspace of at least
- * gsa_indexer_select_workspace_bytes(B, T) bytes (16-byte aligned),
- * overwritten by each call: the causal score tiles, stored once and read
- * back instead of recomputed (B * G(G+1)/2 KiB, G = ceil(T/16)), and the
- * threshold candidates of each 16-row group (B * G * 128 KiB).
- * Supported: Hi == 4, di == 64, 1 <= k_eff <= T.
+ * No score is stored: a sample of every fourth key tile places a band around
+ * each row's k-th score, one exact pass writes the sure winners into the mask
+ * and keeps the band's keys as candidates, and a row whose counts do not
+ * prove the band is selected by an exact radix select over recomputed scores.
+ * The candidates stay in LDS.  ws: caller-provided device workspace of at
+ * least gsa_indexer_select_workspace_bytes(B, T) bytes (16-byte aligned),
+ * overwritten by each call: 512 bytes of store slots per 16-row group
+ * (B * ceil(T/16) * 512 bytes).
+ * Supported: Hi == 4, di == 64, 1 <= k_eff <= T <= 65536.
  */
 size_t gsa_indexer_select_workspace_bytes(int B, int T);
 
@@ -162,14 +165,24 @@ int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
  * row t: the count selected keys ascending, then t+1, t+2, ... up to entry
  * k_t - 1 (present only when t+1 < k_t), then index 0 up to the width, so
  * every entry lies in [0, T)); optionally k_out int32 [B*T] (k_t) and var_out float [B*T] (var_t).
- * Three launches on the stream (scores + variances; the global mean and k_t;
- * the select), all in stream order.  ws: at least
+ * Three launches on the stream (sample histograms + variances; the global
+ * mean and k_t; the select), all in stream order.  ws: at least
  * gsa_indexer_select_adaptive_workspace_bytes(B, T) bytes (16-byte aligned):
- * gsa_indexer_select's workspace, the per-row histograms kept between the
- * launches (B * G * 16 KiB for T <= 65535, twice that above), and room for
- * var and k.  Supported: Hi == 4, di == 64, 1 <= k_min <= k_max, k_base >= 1.
+ * gsa_indexer_select's workspace, the per-row sample histograms kept between
+ * the launches (B * ceil(T/16) * 32 KiB), and room for var and k.
+ * Supported: Hi == 4, di == 64, 1 <= k_min <= k_max, k_base >= 1,
+ * T <= 65536.
  */
 size_t gsa_indexer_select_adaptive_workspace_bytes(int B, int T);
+
+/*
+ * Test hook, no counterpart in the reference: while on != 0, every row of
+ * gsa_indexer_select / gsa_indexer_select_adaptive that has more causal keys
+ * than its k takes the exact fallback path (radix select over recomputed
+ * scores) instead of the sampled band, so that tests can check that path on
+ * ordinary inputs.  Process-wide; returns the previous setting.
+ */
+int gsa_debug_force_select_fallback(int on);
 
 int gsa_indexer_select_adaptive(const void* q_idx, int64_t q_sb, int64_t q_st,
                                 const void* k_idx, int64_t k_sb, int64_t k_st,

@@ -77,7 +77,7 @@ def test_indexer_scores_validation(lib):
     assert _scores(lib, qst=260) == 4        # row stride not a multiple of 8 bf16
 
 
-NWS_T32 = 3 * 1024 + 2 * 16 * 1024 * 8    # indexer-select workspace at B=1, T=32
+NWS_T32 = 2 * 512    # indexer-select workspace at B=1, T=32: two 16-row groups' store slots
 
 
 def _select(lib, **kw):
@@ -103,12 +103,12 @@ def test_indexer_select_validation(lib):
     assert _select(lib, ws=None) == 1
     assert _select(lib, nws=NWS_T32 - 1) == 2     # workspace too small
     assert _select(lib, ws=P + 8) == 4
-    # one 1 KiB score tile per causal (16-row group, 16-key tile) pair, then
-    # 16 rows x 1024 (key, index) candidate slots of 8 bytes per 16-row group
-    cand = 16 * 1024 * 8
-    assert lib.gsa_indexer_select_workspace_bytes(1, 32) == NWS_T32 == 3 * 1024 + 2 * cand
-    assert lib.gsa_indexer_select_workspace_bytes(2, 100) == 2 * (28 * 1024 + 7 * cand)
-    assert lib.gsa_indexer_select_workspace_bytes(1, 65536) == 4096 * 4097 // 2 * 1024 + 4096 * cand
+    assert _select(lib, T=65537, k_eff=8, bst=2 * 1025, nws=1 << 30) == 2   # past the fused selector's largest T
+    # the candidate lists live in LDS: per 16-row group the workspace holds
+    # only 64 8-byte store slots -- linear in T, 2 MiB at T = 65536
+    assert lib.gsa_indexer_select_workspace_bytes(1, 32) == NWS_T32 == 2 * 512
+    assert lib.gsa_indexer_select_workspace_bytes(2, 100) == 2 * 7 * 512
+    assert lib.gsa_indexer_select_workspace_bytes(1, 65536) == 4096 * 512
     assert lib.gsa_indexer_select_workspace_bytes(0, 5) == 0
 
 
@@ -124,16 +124,16 @@ def _adaptive(lib, **kw):
 
 
 # adaptive workspace at B=1, T=32, each part rounded up to 256 bytes: the fixed
-# selector's, the phase-1 histograms (2 groups x 16 rows x 257 packed words),
-# then var and k (128 B each)
-NWS_A32 = NWS_T32 + (2 * 16 * 257 * 4 + 255) // 256 * 256 + 2 * 256
+# selector's, the sample histograms (2 groups x 16 rows x 513 words of two
+# 16-bit counts), then var and k (128 B each)
+NWS_A32 = NWS_T32 + (2 * 16 * 513 * 4 + 255) // 256 * 256 + 2 * 256
 
 
 def test_indexer_select_adaptive_validation(lib):
     assert lib.gsa_indexer_select_adaptive_workspace_bytes(1, 32) == NWS_A32
-    hist_unpacked = 4096 * 16 * 513 * 4       # T = 65536: 32-bit counts
+    hist = 4096 * 16 * 513 * 4
     fixed = lib.gsa_indexer_select_workspace_bytes(1, 65536)
-    assert lib.gsa_indexer_select_adaptive_workspace_bytes(1, 65536) == fixed + hist_unpacked + 2 * 65536 * 4
+    assert lib.gsa_indexer_select_adaptive_workspace_bytes(1, 65536) == fixed + hist + 2 * 65536 * 4
     assert lib.gsa_indexer_select_adaptive_workspace_bytes(0, 8) == 0
     assert _adaptive(lib, bias=None) == 1
     assert _adaptive(lib, ws=None) == 1

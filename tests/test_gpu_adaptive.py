@@ -113,16 +113,24 @@ def _bits_sets(bits):
     return un
 
 
+@pytest.mark.parametrize("forced", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("B,T,k_base,k_min,k_max", [(2, 600, 64, 16, 160), (1, 2100, 256, 64, 700),
-                                                    (4, 129, 32, 8, 64)])
-def test_indexer_select_adaptive_vs_oracle(dev, dtype, B, T, k_base, k_min, k_max):
-    _log(f"indexer_select_adaptive dtype={dtype} B={B} T={T} k=({k_base},{k_min},{k_max})")
+                                                    (4, 129, 32, 8, 64), (1, 4100, 1024, 256, 2048)])
+def test_indexer_select_adaptive_vs_oracle(dev, dtype, B, T, k_base, k_min, k_max, forced):
+    """forced: every row with more keys than its k_t takes the fused selector's exact
+    fallback path instead of the sampled band."""
+    _log(f"indexer_select_adaptive dtype={dtype} B={B} T={T} k=({k_base},{k_min},{k_max}) forced={forced}")
     buf, bias = _indexer_inputs(B, T, dtype, seed=B * 7 + T)
     bd = buf.to(dev)
     qd = bd[..., :256].view(B, T, 4, 64)
     kd, wd, bias_d = bd[..., 256:320], bd[..., 320:324], bias.to(dev)
-    bits, idx, cnt, k_rows, var = _abi.indexer_select_adaptive(qd, kd, wd, bias_d, 0.125, k_base, k_min, k_max)
+    prev = _abi.load().gsa_debug_force_select_fallback(int(forced))
+    try:
+        bits, idx, cnt, k_rows, var = _abi.indexer_select_adaptive(qd, kd, wd, bias_d, 0.125, k_base, k_min,
+                                                                   k_max)
+    finally:
+        _abi.load().gsa_debug_force_select_fallback(prev)
     # the fused kernel's scores are bit-identical to the score kernel's
     S = _abi.indexer_scores(qd, kd, wd, bias_d, 0.125).cpu()
     k_rows, var, idx, cnt = k_rows.cpu(), var.cpu(), idx.cpu(), cnt.cpu()

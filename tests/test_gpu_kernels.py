@@ -114,17 +114,34 @@ def _bits_to_sets(bits):
     return [[set(np.nonzero(unpacked[b, t])[0].tolist()) for t in range(T)] for b in range(B)]
 
 
+class _NoForce:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+
+def _select_mode(forced):
+    """The fused selector's normal path (sampled band, candidates, resolve) or,
+    forced, its exact fallback (radix select over recomputed scores)."""
+    return _abi.forced_select_fallback() if forced else _NoForce()
+
+
+@pytest.mark.parametrize("forced", [False, True])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,T,k", [(1, 48, 16), (2, 33, 8), (1, 512, 256), (1, 1000, 100), (3, 130, 129),
-                                   (1, 2100, 700)])
-def test_indexer_select_equals_scores_then_topk(dev, dtype, B, T, k):
-    """The fused kernel selects exactly what the score kernel + selector select."""
-    _log(f"indexer_select fused==unfused dtype={dtype} B={B} T={T} k={k}")
+                                   (1, 2100, 700), (1, 4100, 2048)])
+def test_indexer_select_equals_scores_then_topk(dev, dtype, B, T, k, forced):
+    """The fused kernel selects exactly what the score kernel + selector select,
+    on its normal path and on its fallback path."""
+    _log(f"indexer_select fused==unfused dtype={dtype} B={B} T={T} k={k} forced_fallback={forced}")
     buf, q, k_, w, bias = _indexer_inputs(B, T, dtype, seed=B * 1000 + T, pad=4)
     bd = buf.to(dev)
     qd = bd[..., :256].view(B, T, 4, 64)
     kd, wd, bias_d = bd[..., 256:320], bd[..., 320:324], bias.to(dev)
-    fb, fi, fc = _abi.indexer_select(qd, kd, wd, bias_d, 0.125, k)
+    with _select_mode(forced):
+        fb, fi, fc = _abi.indexer_select(qd, kd, wd, bias_d, 0.125, k)
     s = _abi.indexer_scores(qd, kd, wd, bias_d, 0.125)
     ui, uc, _ = _abi.topk_select(s, k, _abi.ORDER_INDEX_ASC)
     assert torch.equal(fc.cpu(), uc.cpu())
@@ -136,16 +153,20 @@ def test_indexer_select_equals_scores_then_topk(dev, dtype, B, T, k):
     assert torch.equal(ui.cpu(), oi) and torch.equal(uc.cpu(), oc)
 
 
-@pytest.mark.parametrize("T,k", [(700, 100), (300, 299), (1500, 40)])
-def test_indexer_select_all_ties_overflow_path(dev, T, k):
-    """q = 0: every score of a row is equal, so one bin holds the whole row and the
-    radix passes resolve it; the lowest indices win."""
-    _log(f"indexer_select all-ties T={T} k={k}")
+@pytest.mark.parametrize("forced", [False, True])
+@pytest.mark.parametrize("T,k", [(700, 100), (300, 299), (1500, 40), (3000, 1000)])
+def test_indexer_select_all_ties_overflow_path(dev, T, k, forced):
+    """q = 0: every score of a row is equal, so the band holds the whole row: short
+    rows resolve the ties among their candidates by index, rows with more keys
+    than the candidate lists hold (T=3000) take the exact fallback; the lowest
+    indices win."""
+    _log(f"indexer_select all-ties T={T} k={k} forced_fallback={forced}")
     buf, q, k_, w, bias = _indexer_inputs(1, T, torch.bfloat16, seed=5, pad=4)
     buf[..., :256] = 0
     bd = buf.to(dev)
     qd = bd[..., :256].view(1, T, 4, 64)
-    fb, fi, fc = _abi.indexer_select(qd, bd[..., 256:320], bd[..., 320:324], bias.to(dev), 0.125, k)
+    with _select_mode(forced):
+        fb, fi, fc = _abi.indexer_select(qd, bd[..., 256:320], bd[..., 320:324], bias.to(dev), 0.125, k)
     fi, fc = fi.cpu(), fc.cpu()
     exp = torch.arange(k, dtype=torch.int32).expand(T, k)
     assert torch.equal(fi[0], exp)
@@ -153,6 +174,27 @@ def test_indexer_select_all_ties_overflow_path(dev, T, k):
     sets = _bits_to_sets(fb)[0]
     for t in range(T):
         assert sets[t] == set(range(min(t + 1, k)))
+
+
+def test_indexer_select_equals_scores_then_topk_T16384(dev):
+    """T=16384, k=2048 on synthetic projections: the fused selection (sampled band,
+    candidates, resolve) is bit-identical to the full score matrix followed by the
+    standalone selector, every row (compared on the GPU)."""
+    T, k = 16384, 2048
+    _log("indexer_select fused==unfused T=16384")
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(1, T, 2048, generator=g).to(torch.bfloat16)
+    W = (torch.randn(328, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    proj = torch.nn.functional.linear(x.to(dev), W.to(dev))
+    q, kk, w = proj[..., :256].view(1, T, 4, 64), proj[..., 256:320], proj[..., 320:324]
+    bias = torch.zeros(4, device=dev)
+    fb, fi, fc = _abi.indexer_select(q, kk, w, bias, 0.125, k)
+    s = _abi.indexer_scores(q, kk, w, bias, 0.125)
+    ui, uc, _ = _abi.topk_select(s, k, _abi.ORDER_INDEX_ASC)
+    del s
+    assert torch.equal(fc, uc)
+    assert torch.equal(fi, ui)
+    assert torch.equal(fb, _abi.selection_mask(ui, T, count=uc))
 
 
 def test_indexer_select_overlap_c2(dev):
