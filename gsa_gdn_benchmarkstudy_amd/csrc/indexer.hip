@@ -237,15 +237,23 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 // and the candidate lists, the only data-dependent writes, live in LDS.
 // ---------------------------------------------------------------------------
 constexpr int kNB = 1024;                 // sample histogram bins per row
-constexpr int kHStride = kNB / 2 + 1;     // words per row: 16-bit counts, two per word, + trash bin kNB
+constexpr int kHStride = kNB / 2 + 1;     // words per row: 16-bit counts, two per word (+1: bank spread)
 constexpr int kGroupWaves = 16;           // waves per 16-row group
 constexpr int kGroupThreads = 64 * kGroupWaves;
-constexpr int kRowCap = 1152;             // candidates per row (LDS)
+// Candidate lists.  Each row has 64 writers -- its four lanes in each of the
+// 16 waves -- and every writer a private list of kPrivCap slots; a writer
+// whose list is full spills into the row's overflow list (kOvfCap slots,
+// filled through an atomic counter).
+constexpr int kPrivCap = 12;
+constexpr int kOvfCap = 384;
+constexpr int kPrivWords = 16 * kPrivCap * 64;   // private slots of the 16 rows: [row][slot][writer]
+constexpr int kRowCap = 64 * kPrivCap + kOvfCap; // candidates per row at most (1152)
 constexpr float kBandZ = 5.f;             // band half-width in standard deviations of the sample rank
 constexpr int kFbStride = 512;            // fallback digit histograms: 16 rows x 512 words
-// LDS words shared by the phases: the sample histograms (16 x kHStride), the
-// candidate keys (16 x kRowCap u32) and positions (16 x kRowCap u16), the
-// fallback's digit histograms (16 x kFbStride).
+// LDS words shared by the phases: the sample histograms (16 x kHStride); the
+// candidate keys (private [16][kPrivCap][64] then overflow [16][kOvfCap], u32)
+// and positions (the same two arrays in u16); the fallback's digit
+// histograms (16 x kFbStride).
 constexpr int kPoolWords = 16 * kRowCap + 8 * kRowCap;
 static_assert(16 * kHStride <= kPoolWords && 16 * kFbStride <= kPoolWords, "LDS pool too small");
 constexpr size_t kPoolBytes = (size_t)kPoolWords * 4;
@@ -354,11 +362,14 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   __shared__ int st_mode[16], st_k[16], st_need[16], st_ties[16];
   __shared__ float st_lo[16], st_hi[16], st_invw[16];
   __shared__ int st_sure[16 * kGroupWaves];
-  __shared__ uint32_t st_cnt[16];
+  __shared__ uint32_t st_cnt[16];                  // overflow-list counters
+  __shared__ uint8_t st_pcnt[16][64];              // private-list lengths [row][writer]
   __shared__ uint32_t st_key[16], st_idx[16];
   __shared__ int st_any[3];                       // any active row, any failed row, any index pass
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // (the wave index is read as a scalar so that tile indices, and the
+  // branches on them, are known to be uniform across the wave)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int g = lane >> 4, lr = lane & 15;
   const int ngroups = (p.T + 15) >> 4;
   const int b = blockIdx.x % p.B;
@@ -369,8 +380,10 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   uint16_t* b16 = reinterpret_cast<uint16_t*>(bbase);
   const int64_t row16 = 2 * b_st;                 // uint16 chunks per row
   const int ntl = rg_idx + 1;                     // causal 16-key tiles 0 .. rg_idx
-  uint32_t* ckey = pool;                          // [16][kRowCap]
-  uint16_t* cpos = reinterpret_cast<uint16_t*>(pool + 16 * kRowCap);   // [16][kRowCap]
+  uint32_t* pkey = pool;                          // private keys [16][kPrivCap][64]
+  uint32_t* okey = pool + kPrivWords;             // overflow keys [16][kOvfCap]
+  uint16_t* ppos = reinterpret_cast<uint16_t*>(pool + 16 * kRowCap);   // positions, same layout
+  uint16_t* opos = ppos + kPrivWords;
   // where a lane's mask word goes: its row's word, or a scratch slot
   uint2* scratch = reinterpret_cast<uint2*>(ws + (int64_t)blockIdx.x * kScratchBytes) + lane;
 
@@ -391,22 +404,15 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   // causal prefix now.  (The zeroing is largest for the lightest groups.)
   // Phase 1 writes no mask.
   const int zend = (rg_idx | 3) + 1;              // chunks up to the end of the 64-key word
-  if (kPhase != 1) {
-    for (int i = tid; i < 16 * zend; i += kGroupThreads) {
-      const int rl = i / zend, tile = i % zend;
-      const int r = r0 + rl;
-      if (r >= p.T) continue;
-      if (tile >= ntl) b16[r * row16 + tile] = 0;
-      else if (st_mode[rl] == kTrivial) b16[r * row16 + tile] = prefix_chunk(r, tile);
-    }
+  if (kPhase != 1 && r0 + wave < p.T) {          // wave w writes row r0 + w
+    const int r = r0 + wave;
+    const bool triv = st_mode[wave] == kTrivial;
+    uint16_t* c16 = b16 + (int64_t)r * row16;
+    for (int tile = (triv ? 0 : ntl) + lane; tile < zend; tile += 64)
+      c16[tile] = tile >= ntl ? (uint16_t)0 : prefix_chunk(r, tile);
     const int W = 2 * ((p.T + 63) >> 6);
-    const int d0 = zend >> 2;                     // first 8-byte pair of words past the 64-key word
-    const int npair = (W >> 1) - d0;
-    for (int i = tid; i < 16 * npair; i += kGroupThreads) {
-      const int rl = i / npair, pr = d0 + i % npair;
-      const int r = r0 + rl;
-      if (r < p.T) reinterpret_cast<uint2*>(bbase + (int64_t)r * b_st)[pr] = uint2{0u, 0u};
-    }
+    uint2* c64 = reinterpret_cast<uint2*>(bbase + (int64_t)r * b_st);
+    for (int pr = (zend >> 2) + lane; pr < (W >> 1); pr += 64) c64[pr] = uint2{0u, 0u};
   }
   __syncthreads();
   if (!st_any[0]) return;
@@ -460,11 +466,15 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   } else {
     for (int i = tid; i < 16 * kHStride; i += kGroupThreads) pool[i] = 0u;
     __syncthreads();
+    // (Rows that are not active count into their own, unused histograms.)
     sweep(4 * wave, [](int t) { return t + 4 * kGroupWaves; }, [&](int t, const float (&sc)[4]) {
+      if (t != ntl - 1) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool valid = act && 16 * t + 4 * g + e <= row;
-        hist_add(hrow, valid ? bin_of(sc[e], inv_w) : kNB);
+        for (int e = 0; e < 4; ++e) hist_add(hrow, bin_of(sc[e], inv_w));
+      } else {                                    // the diagonal tile: keys up to the row
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (4 * g + e <= lr) hist_add(hrow, bin_of(sc[e], inv_w));
       }
     });
   }
@@ -495,10 +505,12 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
     __syncthreads();
     const float c = st_c[lr];
     float s1 = 0.f, s2 = 0.f;
+    // (every row below T is active in this phase; the others are not stored)
     sweep(wave, round_robin, [&](int t, const float (&sc)[4]) {
+      const bool diag = t == ntl - 1;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float d = (act && 16 * t + 4 * g + e <= row) ? sc[e] - c : 0.f;
+        const float d = (!diag || 4 * g + e <= lr) ? sc[e] - c : 0.f;
         s1 += d;
         s2 = __builtin_fmaf(d, d, s2);
       }
@@ -567,29 +579,57 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   __syncthreads();   // the histograms are dead from here: the pool holds the candidate lists
 
   // ---- main pass: sure winners -> mask words, band -> candidate lists ---------
+  // A candidate is kept as the bits of its score (scores are sums of
+  // products of sigmoids: never negative, and candidates are never NaN, so
+  // the bits order as the values do once -0 is folded into +0) and its key
+  // index.  The lane is writer (4*wave + g + lr) mod 64 of its row: one
+  // wave's 16 rows then store to 16 different banks.
   {
-    const float lo = act ? st_lo[lr] : __builtin_inff();
+    const float lo = act ? st_lo[lr] : __builtin_nanf("");   // NaN: never a candidate
     const float hi = act ? st_hi[lr] : __builtin_inff();
     uint2* wdst = (g == 0 && act) ? reinterpret_cast<uint2*>(bbase + (int64_t)row * b_st) : nullptr;
-    uint32_t* mykey = ckey + lr * kRowCap;
-    uint16_t* mypos = cpos + lr * kRowCap;
+    const int writer = (4 * wave + g + lr) & 63;
+    uint32_t* pk = pkey + lr * (kPrivCap * 64) + writer;    // slot i at pk[64 * i]
+    uint16_t* pp = ppos + lr * (kPrivCap * 64) + writer;
+    int pc = 0;                                   // candidates of this writer, spilled ones included
     int nsure = 0;
-    // One tile's scores -> sure bits in w2, candidates appended to the row's list.
+    // One tile's scores -> sure bits in w2, candidates into the lists.  The
+    // short form serves tiles below the diagonal while every writer of the
+    // wave has room for four more.
     auto classify = [&](int t, int u, const float (&sc)[4], uint32_t (&w2)[2]) {
+      const int col0 = 16 * t + 4 * g;
       const bool diag = t == ntl - 1;
+      if (!diag && __builtin_amdgcn_ballot_w64(pc > kPrivCap - 4) == 0) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float s = sc[e];
-        const bool valid = act && (!diag || 4 * g + e <= lr);
-        const bool le = s <= hi;
-        const bool sure = valid && !le;               // NaN ranks above every number
-        const bool cand = valid && le && s >= lo;
-        w2[u >> 1] |= sure ? (1u << (16 * (u & 1) + 4 * g + e)) : 0u;
-        if (cand) {
-          const uint32_t at = atomicAdd(&st_cnt[lr], 1u);
-          if (at < (uint32_t)kRowCap) {
-            mykey[at] = score_key(s);
-            mypos[at] = (uint16_t)(16 * t + 4 * g + e);
+        for (int e = 0; e < 4; ++e) {
+          const float s = sc[e];
+          const bool le = s <= hi;
+          w2[u >> 1] |= le ? 0u : (1u << (16 * (u & 1) + 4 * g + e));   // NaN ranks above every number
+          if (le && s >= lo) {
+            pk[64 * pc] = __float_as_uint(s);
+            pp[64 * pc] = (uint16_t)(col0 + e);
+            ++pc;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float s = sc[e];
+          const bool valid = !diag || 4 * g + e <= lr;
+          const bool le = s <= hi;
+          w2[u >> 1] |= (valid && !le) ? (1u << (16 * (u & 1) + 4 * g + e)) : 0u;
+          if (valid && le && s >= lo) {
+            if (pc < kPrivCap) {
+              pk[64 * pc] = __float_as_uint(s);
+              pp[64 * pc] = (uint16_t)(col0 + e);
+            } else {
+              const uint32_t at = atomicAdd(&st_cnt[lr], 1u);
+              if (at < (uint32_t)kOvfCap) {
+                okey[lr * kOvfCap + at] = __float_as_uint(s);
+                opos[lr * kOvfCap + at] = (uint16_t)(col0 + e);
+              }
+            }
+            ++pc;
           }
         }
       }
@@ -600,12 +640,13 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
       *dst = uint2{lo32, hi32};
       nsure += __popc(lo32) + __popc(hi32);
     };
-    // Complete quads of this wave (wave, wave + 16, ...): even tiles of a quad
-    // use key buffer A, odd ones B.  Every turn issues the same memory
-    // operations -- four key-tile loads and one word store -- and the loop is
-    // entered after one load and one (scratch) store, so the compiler's wait
-    // for a buffer always leaves the other buffer's load in flight.
-    const int nfull = ntl >> 2;
+    // Quads of this wave (wave, wave + 16, ...) that lie below the diagonal
+    // tile: even tiles of a quad use key buffer A, odd ones B.  Every turn
+    // issues the same memory operations -- four key-tile loads and one word
+    // store -- and the loop is entered after one load and one (scratch)
+    // store, so the compiler's wait for a buffer always leaves the other
+    // buffer's load in flight.
+    const int nfull = (ntl - 1) >> 2;
     Op kA[kS], kB[kS];
     rgp.load_keys(16 * min(4 * wave, ntl - 1), p.T, lane, kA);
     *scratch = uint2{0u, 0u};
@@ -627,10 +668,11 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
       classify(t0 + 3, 3, sc, w2);
       put_word(qd, w2);
     }
-    // The last, partial quad (1-3 tiles) belongs to wave nfull % 16.
-    if ((ntl & 3) && wave == nfull % kGroupWaves) {
+    // The last quad (1-4 tiles, the diagonal tile among them) belongs to
+    // wave nfull % 16.
+    if (wave == nfull % kGroupWaves) {
       uint32_t w2[2] = {0u, 0u};
-      for (int u = 0; u < (ntl & 3); ++u) {
+      for (int u = 0; u < ntl - 4 * nfull; ++u) {
         const int t = 4 * nfull + u;
         Op kb[kS];
         rgp.load_keys(16 * t, p.T, lane, kb);
@@ -641,6 +683,7 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
       put_word(nfull, w2);
     }
     if (g == 0) st_sure[lr * kGroupWaves + wave] = act ? nsure : 0;
+    st_pcnt[lr][writer] = (uint8_t)min(pc, kPrivCap);
   }
   // The resolve ORs winners into the words stored above, by atomics that
   // execute in L2, from other waves.  A workgroup-scope barrier does not wait
@@ -657,18 +700,30 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
       int n_sure = 0;
 #pragma unroll
       for (int w = 0; w < kGroupWaves; ++w) n_sure += st_sure[rl * kGroupWaves + w];
-      const int n_all = (int)st_cnt[rl];
+      // lane j reads writer j's private list, and every 64th overflow slot
+      const int np = st_pcnt[rl][lane];
+      const int n_ovf = (int)st_cnt[rl];
+      int n_all = np;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) n_all += __shfl_xor(n_all, o, 64);
+      n_all += n_ovf;
       int need = st_k[rl] - n_sure;
-      if (sa.force_fallback || n_all > kRowCap || need < 0 || n_all < need) {
+      if (sa.force_fallback || n_ovf > kOvfCap || need < 0 || n_all < need) {
         if (lane == 0) { st_mode[rl] = kFailed; st_any[1] = 1; }
       } else if (need > 0) {
-        const uint32_t* lk = ckey + rl * kRowCap;
-        const uint16_t* lp = cpos + rl * kRowCap;
-        const int n = n_all;
+        const uint32_t* rk = pkey + rl * (kPrivCap * 64) + lane;
+        const uint16_t* rp = ppos + rl * (kPrivCap * 64) + lane;
+        const uint32_t* xk = okey + rl * kOvfCap;
+        const uint16_t* xp = opos + rl * kOvfCap;
+        // f(key, index) for each of the row's candidates held by this lane
+        auto each = [&](auto&& f) {
+          for (int i = 0; i < np; ++i) f(rk[64 * i] & 0x7fffffffu, (int)rp[64 * i]);
+          for (int i = lane; i < n_ovf; i += 64) f(xk[i] & 0x7fffffffu, (int)xp[i]);
+        };
         // theta = the need-th largest candidate key, MSB-first over the bits on
         // which the candidates differ, 8-bit digits counted in LDS.
         uint32_t kor = 0u, kand = ~0u;
-        for (int i = lane; i < n; i += 64) { kor |= lk[i]; kand &= lk[i]; }
+        each([&](uint32_t kk, int) { kor |= kk; kand &= kk; });
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
           kor |= (uint32_t)__shfl_xor((int)kor, o, 64);
@@ -684,10 +739,9 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
 #pragma unroll
           for (int i = 0; i < 4; ++i) rh[4 * lane + i] = 0u;
           wave_lds_sync();
-          for (int i = lane; i < n; i += 64) {
-            const uint32_t kk = lk[i];
+          each([&](uint32_t kk, int) {
             if ((kk & hmask) == prefix) atomicAdd(&rh[(kk >> shift) & ((1u << nb) - 1u)], 1u);
-          }
+          });
           wave_lds_sync();
           int cb[4], vsum = 0;
 #pragma unroll
@@ -707,7 +761,7 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
         }
         const uint32_t theta = prefix;
         int ties = 0;
-        for (int i = lane; i < n; i += 64) ties += lk[i] == theta ? 1 : 0;
+        each([&](uint32_t kk, int) { ties += kk == theta ? 1 : 0; });
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) ties += __shfl_xor(ties, o, 64);
         uint32_t istar = 0xffffffffu;
@@ -718,14 +772,12 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
 #pragma unroll
             for (int i = 0; i < 4; ++i) rh[4 * lane + i] = 0u;   // 512 digits as 16-bit counts
             wave_lds_sync();
-            for (int i = lane; i < n; i += 64) {
-              if (lk[i] != theta) continue;
-              const int ix = lp[i];
-              if (lvl == 0 || ((uint32_t)ix >> 9) == ip) {
+            each([&](uint32_t kk, int ix) {
+              if (kk == theta && (lvl == 0 || ((uint32_t)ix >> 9) == ip)) {
                 const int dg = (ix >> shift) & 511;
                 atomicAdd(&rh[dg >> 1], 1u << (16 * (dg & 1)));
               }
-            }
+            });
             wave_lds_sync();
             int cb[8], vsum = 0;
 #pragma unroll
@@ -748,11 +800,9 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
           istar = ip;
         }
         uint32_t* brow = bbase + (int64_t)(r0 + rl) * b_st;
-        for (int i = lane; i < n; i += 64) {
-          const uint32_t kk = lk[i];
-          const int ix = lp[i];
+        each([&](uint32_t kk, int ix) {
           if (kk > theta || (kk == theta && (uint32_t)ix <= istar)) atomicOr(&brow[ix >> 5], 1u << (ix & 31));
-        }
+        });
       }
     }
   }
