@@ -39,6 +39,7 @@ EXPORTS = (
     "gsa_indexer_select_adaptive_workspace_bytes", "gsa_topk_select_adaptive",
     "gsa_proj_packed_bytes", "gsa_proj_pack", "gsa_proj_fused", "gsa_dense_lane_masks",
     "gsa_prologue_vt_lane_masks", "gsa_debug_force_select_fallback",
+    "gsa_indexer_select_noalloc", "gsa_indexer_select_noalloc_max_bytes",
 )
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -55,6 +56,10 @@ _PROTOS = {
                             _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp,
                             _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_indexer_select_workspace_bytes": ([_i32, _i32], ctypes.c_size_t),
+    "gsa_indexer_select_noalloc": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
+                                    _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp,
+                                    _vp], _i32),
+    "gsa_indexer_select_noalloc_max_bytes": ([], ctypes.c_size_t),
     "gsa_indexer_select_adaptive": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _f32,
                                      _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                      _vp, _i64, _i64, _vp, _vp, _vp, _vp,
@@ -265,6 +270,25 @@ def indexer_select(q_idx, k_idx, w, bias32, scale: float, k_eff: int, indices: b
                                 _ptr(ws), nbytes, _stream(q_idx))
     _check(st, "gsa_indexer_select")
     return bits, idx, cnt
+
+
+def indexer_select_noalloc(q_idx, k_idx, w, bias32, scale: float, k_eff: int, bits: torch.Tensor,
+                           idx: Optional[torch.Tensor] = None, cnt: Optional[torch.Tensor] = None) -> None:
+    """gsa_indexer_select_noalloc: indexer_select into caller-given outputs
+    (bits int32 [B,T,W]; optional idx int32 [B,T,k_eff] and cnt int32 [B,T])
+    with no workspace -- the library's static device array stands in for it,
+    so B * ceil(T/16) is limited (GSA_ERR_SCRATCH beyond).  Allocates nothing."""
+    lib = load()
+    _need_cuda(q_idx, k_idx, w, bias32, bits, idx, cnt)
+    B, T, Hi, di = q_idx.shape
+    _expect(tuple(bits.shape) == (B, T, mask_words(T)) and bits.is_contiguous(), "bits: contiguous [B,T,W]")
+    _expect((idx is None) == (cnt is None), "idx and cnt go together")
+    qs, ks, wst = _rows(q_idx, Hi * di), _rows(k_idx, di), _rows(w, Hi)
+    st = lib.gsa_indexer_select_noalloc(_ptr(q_idx), *qs, _ptr(k_idx), *ks, _ptr(w), *wst, _ptr(bias32),
+                                        float(scale), B, T, Hi, di, int(k_eff), dtype_code(q_idx.dtype),
+                                        _ptr(bits), bits.stride(0), bits.stride(1), _ptr(idx), _ptr(cnt),
+                                        _stream(q_idx))
+    _check(st, "gsa_indexer_select_noalloc")
 
 
 class forced_select_fallback:

@@ -12,6 +12,7 @@ extern "C" const char* gsa_status_string(int status) {
     case GSA_ERR_ALIGN: return "pointer or stride breaks the 16-byte vector-load alignment";
     case GSA_ERR_K: return "k out of range";
     case GSA_ERR_FLAGS: return "unknown flag or order code";
+    case GSA_ERR_SCRATCH: return "sizes exceed the static scratch of gsa_indexer_select_noalloc";
     default: break;
   }
   return status < 0 ? "HIP launch error (negated hipError_t)" : "unknown status";

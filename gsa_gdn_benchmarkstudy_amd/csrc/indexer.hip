@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 // that the compiler cannot count.  So the tile loops issue a fixed number of
 // vector memory instructions per tile -- key loads two tiles ahead,
 // unconditional (clamped to the last tile), and one unconditional mask-word
-// store per quad (lanes with nothing to write store to a scratch slot) --
+// store per quad (lanes with nothing to write store to a sink slot) --
 // and the candidate lists, the only data-dependent writes, live in LDS.
 // ---------------------------------------------------------------------------
 constexpr int kNB = 1024;                 // sample histogram bins per row
@@ -257,7 +257,7 @@ constexpr int kFbStride = 512;            // fallback digit histograms: 16 rows 
 constexpr int kPoolWords = 16 * kRowCap + 8 * kRowCap;
 static_assert(16 * kHStride <= kPoolWords && 16 * kFbStride <= kPoolWords, "LDS pool too small");
 constexpr size_t kPoolBytes = (size_t)kPoolWords * 4;
-constexpr size_t kScratchBytes = 64 * 8;  // per 16-row group: the mask-word store slots of non-writing lanes
+constexpr size_t kSinkBytes = 64 * 8;     // per 16-row group: the mask-word store slots of non-writing lanes
 // A candidate's key index is kept in 16 bits (and the 16-bit sample counts
 // hold at most 16 * ceil(T/64) keys per row).
 constexpr int kMaxSelectT = 65536;
@@ -384,8 +384,8 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   uint32_t* okey = pool + kPrivWords;             // overflow keys [16][kOvfCap]
   uint16_t* ppos = reinterpret_cast<uint16_t*>(pool + 16 * kRowCap);   // positions, same layout
   uint16_t* opos = ppos + kPrivWords;
-  // where a lane's mask word goes: its row's word, or a scratch slot
-  uint2* scratch = reinterpret_cast<uint2*>(ws + (int64_t)blockIdx.x * kScratchBytes) + lane;
+  // where a lane's mask word goes: its row's word, or a sink slot
+  uint2* sink = reinterpret_cast<uint2*>(ws + (int64_t)blockIdx.x * kSinkBytes) + lane;
 
   if (tid < 16) {
     const int r = r0 + tid;
@@ -636,20 +636,20 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
     };
     auto put_word = [&](int qd, const uint32_t (&w2)[2]) {
       const uint32_t lo32 = or_row4(w2[0]), hi32 = or_row4(w2[1]);
-      uint2* dst = wdst ? wdst + qd : scratch;
+      uint2* dst = wdst ? wdst + qd : sink;
       *dst = uint2{lo32, hi32};
       nsure += __popc(lo32) + __popc(hi32);
     };
     // Quads of this wave (wave, wave + 16, ...) that lie below the diagonal
     // tile: even tiles of a quad use key buffer A, odd ones B.  Every turn
     // issues the same memory operations -- four key-tile loads and one word
-    // store -- and the loop is entered after one load and one (scratch)
+    // store -- and the loop is entered after one load and one (sink)
     // store, so the compiler's wait for a buffer always leaves the other
     // buffer's load in flight.
     const int nfull = (ntl - 1) >> 2;
     Op kA[kS], kB[kS];
     rgp.load_keys(16 * min(4 * wave, ntl - 1), p.T, lane, kA);
-    *scratch = uint2{0u, 0u};
+    *sink = uint2{0u, 0u};
     for (int qd = wave; qd < nfull; qd += kGroupWaves) {
       uint32_t w2[2] = {0u, 0u};
       const int t0 = 4 * qd;
@@ -898,7 +898,7 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
         }
       }
       const uint32_t lo32 = or_row4(w2[0]), hi32 = or_row4(w2[1]);
-      uint2* dst = wdst ? wdst + qd : scratch;
+      uint2* dst = wdst ? wdst + qd : sink;
       *dst = uint2{lo32, hi32};
     }
   }
@@ -993,9 +993,21 @@ __global__ __launch_bounds__(1024) void adaptive_k_kernel(const float* __restric
 }  // namespace gsa
 
 // ---------------------------------------------------------------------------
+// Device memory of gsa_indexer_select_noalloc: the selector's sink slots
+// (kSinkBytes per 16-row group) for callers that cannot allocate.  Every
+// device that loads the library holds one copy, at its own address, until
+// the process ends.  Host code never passes `scratch` itself to a kernel
+// (in host code it names a host-side stand-in): it takes each device's
+// address from hipGetSymbolAddress once and passes that.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;   // B * ceil(T/16) <= 8192 groups
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// ---------------------------------------------------------------------------
 // Host entry points
 // ---------------------------------------------------------------------------
 #include <atomic>
+#include <mutex>
 
 using namespace gsa_host;
 
@@ -1091,10 +1103,10 @@ static int launch_select(const gsa::IdxArgs& a, gsa::SelArgs sa, int dtype, uint
 }
 
 // The candidate lists live in LDS: the workspace holds only the store slots of
-// lanes without a mask word to write (kScratchBytes per 16-row group).
+// lanes without a mask word to write (kSinkBytes per 16-row group).
 extern "C" size_t gsa_indexer_select_workspace_bytes(int B, int T) {
   if (B < 1 || T < 1) return 0;
-  return (size_t)B * (size_t)((T + 15) / 16) * gsa::kScratchBytes;
+  return (size_t)B * (size_t)((T + 15) / 16) * gsa::kSinkBytes;
 }
 
 extern "C" int gsa_debug_force_select_fallback(int on) {
@@ -1112,10 +1124,10 @@ int gsa_host::launch_adaptive_k(const float* var, int n, int k_base, int k_min, 
 static int check_select_args(const void* q_idx, int64_t q_sb, int64_t q_st, const void* k_idx, int64_t k_sb,
                              int64_t k_st, const void* w, const float* bias, int B, int T, int Hi, int di,
                              int dtype, const uint32_t* bits, int64_t b_sb, int64_t b_st,
-                             const int32_t* idx_out, const int32_t* count_out, const void* ws) {
+                             const int32_t* idx_out, const int32_t* count_out) {
   int st = check_indexer_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype);
   if (st) return st;
-  if (!bits || !ws) return GSA_ERR_NULL;
+  if (!bits) return GSA_ERR_NULL;
   if ((idx_out == nullptr) != (count_out == nullptr)) return GSA_ERR_NULL;
   if (T > gsa::kMaxSelectT) return GSA_ERR_SHAPE;
   const int W = 2 * ((T + 63) / 64);
@@ -1123,8 +1135,19 @@ static int check_select_args(const void* q_idx, int64_t q_sb, int64_t q_st, cons
   if (!aligned(bits, 8) || (b_st % 2) || (b_sb % 2)) return GSA_ERR_ALIGN;
   if (idx_out && (!aligned(idx_out, 4) || !aligned(count_out, 4))) return GSA_ERR_ALIGN;
   if ((int64_t)B * T > 0x7fffffffLL) return GSA_ERR_SHAPE;
-  if (!aligned(ws, 16)) return GSA_ERR_ALIGN;
   return GSA_OK;
+}
+
+// The launches of the fixed-k select, after its arguments are checked; ws
+// holds at least gsa_indexer_select_workspace_bytes(B, T) bytes.
+static int select_fixed(const gsa::IdxArgs& a, int k_eff, int dtype, uint32_t* bits, int64_t b_sb,
+                        int64_t b_st, int32_t* idx_out, int32_t* count_out, uint8_t* ws, hipStream_t s) {
+  int st = launch_select<0>(a, gsa::SelArgs{k_eff, nullptr, nullptr, nullptr, 0}, dtype, bits, b_sb, b_st, ws, s);
+  if (st || !idx_out) return st;
+  const int W = 2 * ((a.T + 63) / 64);
+  hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(a.B * a.T), dim3(256), 0, s, bits, b_sb, b_st, a.T, W,
+                     k_eff, nullptr, idx_out, count_out);
+  return launch_status();
 }
 
 extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
@@ -1136,19 +1159,57 @@ extern "C" int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                                   int32_t* idx_out, int32_t* count_out,
                                   void* ws, size_t ws_bytes, void* stream) {
   int st = check_select_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype, bits, b_sb,
-                             b_st, idx_out, count_out, ws);
+                             b_st, idx_out, count_out);
   if (st) return st;
+  if (!ws) return GSA_ERR_NULL;
+  if (!aligned(ws, 16)) return GSA_ERR_ALIGN;
   if (k_eff < 1 || k_eff > T) return GSA_ERR_K;
   if (ws_bytes < gsa_indexer_select_workspace_bytes(B, T)) return GSA_ERR_SHAPE;
   gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  st = launch_select<0>(a, gsa::SelArgs{k_eff, nullptr, nullptr, nullptr, 0}, dtype, bits, b_sb, b_st,
-                        static_cast<uint8_t*>(ws), s);
-  if (st || !idx_out) return st;
-  const int W = 2 * ((T + 63) / 64);
-  hipLaunchKernelGGL(gsa::bits_to_indices_kernel, dim3(B * T), dim3(256), 0, s, bits, b_sb, b_st, T, W, k_eff,
-                     nullptr, idx_out, count_out);
-  return launch_status();
+  return select_fixed(a, k_eff, dtype, bits, b_sb, b_st, idx_out, count_out, static_cast<uint8_t*>(ws),
+                      static_cast<hipStream_t>(stream));
+}
+
+// Each device's address of `scratch`, looked up on the first call of
+// gsa_indexer_select_noalloc with that device current.
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+static int noalloc_scratch(uint8_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return GSA_ERR_SHAPE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return -static_cast<int>(e);
+    if (!ptr) return -static_cast<int>(hipErrorInvalidSymbol);
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return GSA_OK;
+}
+
+extern "C" size_t gsa_indexer_select_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int gsa_indexer_select_noalloc(const void* q_idx, int64_t q_sb, int64_t q_st,
+                                          const void* k_idx, int64_t k_sb, int64_t k_st,
+                                          const void* w, int64_t w_sb, int64_t w_st,
+                                          const float* bias, float scale,
+                                          int B, int T, int Hi, int di, int k_eff, int dtype,
+                                          uint32_t* bits, int64_t b_sb, int64_t b_st,
+                                          int32_t* idx_out, int32_t* count_out, void* stream) {
+  int st = check_select_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype, bits, b_sb,
+                             b_st, idx_out, count_out);
+  if (st) return st;
+  if (k_eff < 1 || k_eff > T) return GSA_ERR_K;
+  if (gsa_indexer_select_workspace_bytes(B, T) > kNoAllocScratchBytes) return GSA_ERR_SCRATCH;
+  uint8_t* ws = nullptr;
+  if ((st = noalloc_scratch(&ws))) return st;
+  gsa::IdxArgs a = make_idx_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, w_sb, w_st, bias, scale, B, T);
+  return select_fixed(a, k_eff, dtype, bits, b_sb, b_st, idx_out, count_out, ws, static_cast<hipStream_t>(stream));
 }
 
 // Adaptive workspace: the fixed selector's, then the sample histograms kept
@@ -1178,8 +1239,10 @@ extern "C" int gsa_indexer_select_adaptive(const void* q_idx, int64_t q_sb, int6
                                            int32_t* k_out, float* var_out,
                                            void* ws, size_t ws_bytes, void* stream) {
   int st = check_select_args(q_idx, q_sb, q_st, k_idx, k_sb, k_st, w, bias, B, T, Hi, di, dtype, bits, b_sb,
-                             b_st, idx_out, count_out, ws);
+                             b_st, idx_out, count_out);
   if (st) return st;
+  if (!ws) return GSA_ERR_NULL;
+  if (!aligned(ws, 16)) return GSA_ERR_ALIGN;
   if (k_base < 1 || k_min < 1 || k_max < k_min) return GSA_ERR_K;
   if ((k_out && !aligned(k_out, 4)) || (var_out && !aligned(var_out, 4))) return GSA_ERR_ALIGN;
   if (ws_bytes < gsa_indexer_select_adaptive_workspace_bytes(B, T)) return GSA_ERR_SHAPE;

@@ -16,7 +16,9 @@
  *    call (indices and counts are int32, masks uint8, scores and bias fp32).
  *  - Ownership: the caller owns every buffer.  The library never allocates,
  *    frees or retains device memory and never synchronises; every call is
- *    enqueued on `stream` and returns.
+ *    enqueued on `stream` and returns.  (The one exception is the static
+ *    device array behind gsa_indexer_select_noalloc: it is part of the loaded
+ *    code object, one copy per device, and lives until the process ends.)
  *  - Errors: 0 on success; > 0 for argument errors, detected on the host
  *    before anything is enqueued; < 0 is the negated hipError_t of a failed
  *    launch.  gsa_status_string() names every code.
@@ -44,6 +46,7 @@ extern "C" {
 #define GSA_ERR_ALIGN     4  /* pointer or stride breaks the vector-load alignment */
 #define GSA_ERR_K         5  /* k out of range (k < 1, k > keys, or too large)     */
 #define GSA_ERR_FLAGS     6  /* unknown flag or order code                         */
+#define GSA_ERR_SCRATCH   7  /* sizes exceed gsa_indexer_select_noalloc's static scratch */
 
 /* Order of gsa_topk_select's output */
 #define GSA_ORDER_INDEX_ASC  0  /* valid indices ascending, then invalid ones ascending */
@@ -150,6 +153,31 @@ int gsa_indexer_select(const void* q_idx, int64_t q_sb, int64_t q_st,
                        int32_t* idx_out, int32_t* count_out,
                        void* ws, size_t ws_bytes,
                        void* stream);
+
+/*
+ * gsa_indexer_select without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, outputs and
+ * checks as gsa_indexer_select minus ws/ws_bytes; its launches use a static
+ * device array of gsa_indexer_select_noalloc_max_bytes() bytes (4 MiB; one
+ * copy per device, held until the process ends) instead, so it accepts only
+ * gsa_indexer_select_workspace_bytes(B, T) <= that, i.e. B * ceil(T/16) <=
+ * 8192 (GSA_ERR_SCRATCH otherwise, before anything is enqueued).  It calls no
+ * allocator.  The first call on a device looks the array's address up on
+ * that device.  Every call on one device shares that device's array: calls
+ * that overlap on one device race on it (the selector only stores discarded
+ * values there, but no result is promised for overlapping calls).
+ */
+size_t gsa_indexer_select_noalloc_max_bytes(void);
+
+int gsa_indexer_select_noalloc(const void* q_idx, int64_t q_sb, int64_t q_st,
+                               const void* k_idx, int64_t k_sb, int64_t k_st,
+                               const void* w, int64_t w_sb, int64_t w_st,
+                               const float* bias, float scale,
+                               int B, int T, int Hi, int di, int k_eff, int dtype,
+                               uint32_t* bits, int64_t b_sb, int64_t b_st,
+                               int32_t* idx_out, int32_t* count_out,
+                               void* stream);
 
 /*
  * The fused indexer + exact top-k with a per-row k from the score variance:

@@ -51,7 +51,7 @@ def test_constants_match_header(lib):
 
 
 def test_status_strings(lib):
-    for code in range(0, 7):
+    for code in range(0, 8):
         assert _abi.status_string(code) not in ("", "unknown status")
     assert "HIP" in _abi.status_string(-1)
     assert _abi.status_string(99) == "unknown status"
@@ -110,6 +110,34 @@ def test_indexer_select_validation(lib):
     assert lib.gsa_indexer_select_workspace_bytes(2, 100) == 2 * 7 * 512
     assert lib.gsa_indexer_select_workspace_bytes(1, 65536) == 4096 * 512
     assert lib.gsa_indexer_select_workspace_bytes(0, 5) == 0
+
+
+def _noalloc(lib, **kw):
+    a = dict(q=P, qsb=0, qst=256, k=P, ksb=0, kst=64, w=P, wsb=0, wst=4, bias=P, scale=0.125,
+             B=1, T=32, Hi=4, di=64, k_eff=8, dtype=1, bits=P, bsb=0, bst=2, idx=P, cnt=P)
+    a.update(kw)
+    return lib.gsa_indexer_select_noalloc(a["q"], a["qsb"], a["qst"], a["k"], a["ksb"], a["kst"], a["w"],
+                                          a["wsb"], a["wst"], a["bias"], a["scale"], a["B"], a["T"], a["Hi"],
+                                          a["di"], a["k_eff"], a["dtype"], a["bits"], a["bsb"], a["bst"],
+                                          a["idx"], a["cnt"], None)
+
+
+def test_indexer_select_noalloc_validation(lib):
+    # the static scratch: 4 MiB = 8192 groups of 16 rows x 512 bytes of store slots
+    assert lib.gsa_indexer_select_noalloc_max_bytes() == 4 << 20
+    assert _abi.status_string(7).startswith("sizes exceed the static scratch")
+    assert _noalloc(lib, bias=None) == 1
+    assert _noalloc(lib, bits=None) == 1
+    assert _noalloc(lib, cnt=None) == 1
+    assert _noalloc(lib, k_eff=0) == 5
+    assert _noalloc(lib, dtype=-1) == 3
+    assert _noalloc(lib, k=MIS) == 4
+    assert _noalloc(lib, bst=1) == 2
+    # 8192 groups fit (B=2, T=65536); one more group does not
+    W = 2 * 1024
+    assert _noalloc(lib, B=4, T=32768 + 1, bst=W, bsb=(32768 + 1) * W) == 7
+    assert _noalloc(lib, B=8193, T=16, bst=2, bsb=32) == 7
+    assert _noalloc(lib, T=65537, bst=2 * 1025) == 2      # past the fused selector's largest T
 
 
 def _adaptive(lib, **kw):
