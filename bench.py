@@ -84,14 +84,36 @@ def profiled_traffic(kernel, config):
     return None
 
 
+def cpu_c1_unchunked(reps=3):
+    """The CPU oracle's unchunked fp32 forward at the reference's own CPU case
+    (B=1, T=512, k_base=256, k_min=64, k_max=512): gsa_ref.py's op sequence,
+    1 warm-up + `reps` timed forwards, as gsa_triton/benchmark.py:179-197 times
+    its GPU runs."""
+    from oracle import gsa_oracle as orc
+
+    cfg = orc.GSAConfig(hidden_size=D, num_heads=H, k_max=512, d_indexer=DI, n_idx_heads=HI,
+                        k_base=256, k_min=64)
+    sd = orc.synthetic_state(cfg, seed=0)
+    x = orc.synthetic_input(1, 512, D, seed=1)
+    with torch.inference_mode():
+        orc.gsa_forward(sd, cfg, x)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            orc.gsa_forward(sd, cfg, x)
+        sec = (time.perf_counter() - t0) / reps
+    return {"workload": f"GSA layer forward B=1 T=512 D={D} H={H} fp32 k_base=256 k_max=512, unchunked",
+            "ms_per_forward": sec * 1e3, "tokens_per_s": 512 / sec, "warmup": 1, "timed": reps}
+
+
 def cpu_baseline(B, T, budget_s, dtype=torch.bfloat16):
     """The CPU oracle (restatement of gsa_ref.py's forward) on sampled query rows
     of the same workload: per-token cost = the token's own projections plus its
     indexer row, selection, gathered attention and o_proj, over row chunks spread
-    evenly across the sequence, until the time budget is spent."""
+    evenly across the sequence, until the time budget is spent.  Every core of
+    the process's affinity set runs torch's intra-op threads."""
     from oracle import gsa_oracle as orc
 
-    ncores = min(len(os.sched_getaffinity(0)), 16)
+    ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
     cfg = orc.GSAConfig(hidden_size=D, num_heads=H, k_max=K_MAX, d_indexer=DI, n_idx_heads=HI,
                         k_base=K_BASE, k_min=K_MIN)
@@ -124,6 +146,8 @@ def cpu_baseline(B, T, budget_s, dtype=torch.bfloat16):
         pass
     return {
         "value": B * done_rows / spent, "unit": "tokens/s", "cores": ncores, "kind": "port",
+        "threads": torch.get_num_threads(),
+        "c1_fp32_unchunked": cpu_c1_unchunked(),
         "sample": (f"CPU oracle (torch restatement of gsa_ref.py forward, {str(dtype).split('.')[-1]}) "
                    f"on {done_rows} of {T} query rows in {done_rows // chunk} chunks of {chunk} spread "
                    f"over the sequence; per row: its 8 projections + indexer row vs all keys + top-k "
@@ -290,24 +314,33 @@ def main():
     aflops = 4 * P * H * DH                     # useful (selected-pair) QK and PV flops
     fidx = indexer_flops(B, T)
     idx_tflops = fidx / (idx_ms * 1e-3) / 1e12
-    gather_roof = {"kernel": "gsa_sparse_attn", "bound": "hbm", "achieved": gather_gbs, "peak": HBM_PEAK_GBS,
-                   "unit": "GB/s", "frac": gather_gbs / HBM_PEAK_GBS,
-                   "traffic": profiled_traffic("gsa_sparse_attn", args.config),
-                   "algorithmic_bytes": abytes, "valid_pairs": P, "ms": gather_ms,
-                   "note": "algorithmic bytes count every selected K/V row as an HBM read; rows that "
-                           "many queries select are served from L2 and the last-level cache, so the "
-                           "rate can exceed the HBM peak"}
+    g_traffic = profiled_traffic("gsa_sparse_attn", args.config)
+    g_rate = None if g_traffic is None else g_traffic / (gather_ms * 1e-3) / 1e9
+    gather_roof = {"kernel": "gsa_sparse_attn", "bound": "hbm", "achieved": g_rate, "peak": HBM_PEAK_GBS,
+                   "unit": "GB/s", "frac": None if g_rate is None else g_rate / HBM_PEAK_GBS,
+                   "traffic": g_traffic, "ms": gather_ms,
+                   "note": "achieved = traffic (rocprofv3 FETCH_SIZE + WRITE_SIZE per launch beyond L2, "
+                           "calibrated on a plain copy; it includes last-level-cache hits, so it bounds "
+                           "the DRAM rate from above) / the kernel time measured here",
+                   "algorithmic_rate": {"value": gather_gbs, "unit": "GB/s", "bytes": abytes, "valid_pairs": P,
+                                        "note": "every selected K/V row counted as one read: rows that "
+                                                "many queries select come from the caches, so this rate "
+                                                "is not an HBM rate and may exceed the HBM peak"}}
     if attn_impl == "dense":
         qrows = 256                              # query rows per block of gsa_dense_attn
         nqb = (T + qrows - 1) // qrows
         dense_flops = 4 * B * H * DH * qrows * 64 * sum(min(qb * qrows + qrows - 1, T - 1) // 64 + 1
                                                          for qb in range(nqb))
         ach = aflops / (attn_ms * 1e-3) / 1e12
+        ex = dense_flops / (attn_ms * 1e-3) / 1e12
         roofline = {"kernel": "gsa_dense_attn", "bound": "mfma", "achieved": ach, "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": ach / BF16_PEAK_TFLOPS,
                     "traffic": profiled_traffic("gsa_dense_attn", args.config),
                     "algorithmic_flops": aflops, "executed_flops": dense_flops,
-                    "executed_tflops": dense_flops / (attn_ms * 1e-3) / 1e12, "ms": attn_ms}
+                    "executed_tflops": ex, "executed_frac": ex / BF16_PEAK_TFLOPS, "ms": attn_ms,
+                    "note": "achieved/frac: the selected (useful) pairs' QK and PV flops; executed: every "
+                            "MFMA the kernel issues (whole 64-key tiles up to the diagonal), the count "
+                            "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 gives"}
     else:
         roofline = gather_roof
 

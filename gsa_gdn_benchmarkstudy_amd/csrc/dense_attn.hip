@@ -163,15 +163,19 @@ __device__ __forceinline__ void lane_mask_block(const LaneMaskArgs& a, int blk) 
     if (kt0 + u >= NT) break;
     const uint64_t word = words[u] >> (8 * h);
     int lo = 0, hi = 0;                      // slot s's mask lands in lane s
+    // A tile no row of the group selects from (every tile past the group's
+    // diagonal, for a causal selection) has all-zero masks: no transpose.
+    if (ballot64(words[u] != 0ull)) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint64_t m = ballot64((word >> (32 * c + 16 * (r >> 3) + (r & 7))) & 1ull);
-        const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (16 * c + r));   // lane == slot
-        lo = mine ? (int)(uint32_t)m : lo;
-        hi = mine ? (int)(uint32_t)(m >> 32) : hi;
-      }
+        for (int r = 0; r < 16; ++r) {
+          const uint64_t m = ballot64((word >> (32 * c + 16 * (r >> 3) + (r & 7))) & 1ull);
+          const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (16 * c + r));   // lane == slot
+          lo = mine ? (int)(uint32_t)m : lo;
+          hi = mine ? (int)(uint32_t)(m >> 32) : hi;
+        }
+    }
     if (lane < 32) lm[((int64_t)bg * NT + kt0 + u) * 32 + lane] = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
   }
 }
