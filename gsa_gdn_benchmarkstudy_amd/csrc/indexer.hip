@@ -136,12 +136,39 @@ struct RowGroup {
     const float den = d01 * d23;
     const float num = __builtin_fmaf(n01, d23, n23 * d01);
     float s = num * __builtin_amdgcn_rcpf(den);
-    if (!(den < 0x1p124f)) {     // also NaN
-      s = a[0] * __builtin_amdgcn_rcpf(1.0f + x[0]);
-#pragma unroll
-      for (int h = 1; h < kHi; ++h) s = __builtin_fmaf(a[h], __builtin_amdgcn_rcpf(1.0f + x[h]), s);
-    }
+    if (!(den < 0x1p124f)) s = per_head(x);   // also NaN
     return s;
+  }
+  __device__ float per_head(const float (&x)[kHi]) const {
+    float s = a[0] * __builtin_amdgcn_rcpf(1.0f + x[0]);
+#pragma unroll
+    for (int h = 1; h < kHi; ++h) s = __builtin_fmaf(a[h], __builtin_amdgcn_rcpf(1.0f + x[h]), s);
+    return s;
+  }
+  // score() of the four slots of a tile, bit for bit, with one range test
+  // for the tile: the sum of the four (positive) denominators is below
+  // 2^124 only if each is, and it is NaN if any is.
+  __device__ void score4(const floatx4 (&acc)[kHi], float (&sc)[4]) const {
+    float x[4][kHi], den[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int h = 0; h < kHi; ++h)
+        x[e][h] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[h][e], scale_l2, bias_l2[h]));
+      const float u0 = 1.0f + x[e][0], u2 = 1.0f + x[e][2];
+      const float d01 = __builtin_fmaf(u0, x[e][1], u0);
+      const float d23 = __builtin_fmaf(u2, x[e][3], u2);
+      const float n01 = __builtin_fmaf(a[1], x[e][0], __builtin_fmaf(a[0], x[e][1], c01));
+      const float n23 = __builtin_fmaf(a[3], x[e][2], __builtin_fmaf(a[2], x[e][3], c23));
+      den[e] = d01 * d23;
+      const float num = __builtin_fmaf(n01, d23, n23 * d01);
+      sc[e] = num * __builtin_amdgcn_rcpf(den[e]);
+    }
+    if (!((den[0] + den[1]) + (den[2] + den[3]) < 0x1p124f)) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (!(den[e] < 0x1p124f)) sc[e] = per_head(x[e]);
+    }
   }
 };
 
@@ -245,8 +272,10 @@ constexpr int kGroupThreads = 64 * kGroupWaves;
 // whose list is full spills into the row's overflow list (kOvfCap slots,
 // filled through an atomic counter).
 constexpr int kPrivCap = 12;
+constexpr int kPrivSlots = kPrivCap + 1;          // + one trash slot per writer (stores of non-candidates)
 constexpr int kOvfCap = 384;
-constexpr int kPrivWords = 16 * kPrivCap * 64;   // private slots of the 16 rows: [row][slot][writer]
+constexpr int kPrivWords = 16 * kPrivSlots * 64; // private slots of the 16 rows: [row][slot][writer]
+constexpr int kKeyWords = kPrivWords + 16 * kOvfCap;
 constexpr int kRowCap = 64 * kPrivCap + kOvfCap; // candidates per row at most (1152)
 constexpr float kBandZ = 5.f;             // band half-width in standard deviations of the sample rank
 constexpr int kFbStride = 512;            // fallback digit histograms: 16 rows x 512 words
@@ -254,7 +283,7 @@ constexpr int kFbStride = 512;            // fallback digit histograms: 16 rows 
 // candidate keys (private [16][kPrivCap][64] then overflow [16][kOvfCap], u32)
 // and positions (the same two arrays in u16); the fallback's digit
 // histograms (16 x kFbStride).
-constexpr int kPoolWords = 16 * kRowCap + 8 * kRowCap;
+constexpr int kPoolWords = kKeyWords + kKeyWords / 2;
 static_assert(16 * kHStride <= kPoolWords && 16 * kFbStride <= kPoolWords, "LDS pool too small");
 constexpr size_t kPoolBytes = (size_t)kPoolWords * 4;
 constexpr size_t kSinkBytes = 64 * 8;     // per 16-row group: the mask-word store slots of non-writing lanes
@@ -380,9 +409,9 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   uint16_t* b16 = reinterpret_cast<uint16_t*>(bbase);
   const int64_t row16 = 2 * b_st;                 // uint16 chunks per row
   const int ntl = rg_idx + 1;                     // causal 16-key tiles 0 .. rg_idx
-  uint32_t* pkey = pool;                          // private keys [16][kPrivCap][64]
+  uint32_t* pkey = pool;                          // private keys [16][kPrivSlots][64]
   uint32_t* okey = pool + kPrivWords;             // overflow keys [16][kOvfCap]
-  uint16_t* ppos = reinterpret_cast<uint16_t*>(pool + 16 * kRowCap);   // positions, same layout
+  uint16_t* ppos = reinterpret_cast<uint16_t*>(pool + kKeyWords);     // positions, same layout
   uint16_t* opos = ppos + kPrivWords;
   // where a lane's mask word goes: its row's word, or a sink slot
   uint2* sink = reinterpret_cast<uint2*>(ws + (int64_t)blockIdx.x * kSinkBytes) + lane;
@@ -435,8 +464,7 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   auto tile = [&](const Op (&kb)[kS], float (&sc)[4]) {
     floatx4 acc[kHi];
     rgp.mma(kb, acc);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sc[e] = rgp.score(acc, e);
+    rgp.score4(acc, sc);
   };
   auto sweep = [&](int first, auto&& next, auto&& f) {
     Op ka[kS], kb[kS];
@@ -582,15 +610,15 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
   // A candidate is kept as the bits of its score (scores are sums of
   // products of sigmoids: never negative, and candidates are never NaN, so
   // the bits order as the values do once -0 is folded into +0) and its key
-  // index.  The lane is writer (4*wave + g + lr) mod 64 of its row: one
-  // wave's 16 rows then store to 16 different banks.
+  // index.  The lane is writer (wave + 16g + lr) mod 64 of its row: the 64
+  // lanes of one wave then store to 64 different banks.
   {
     const float lo = act ? st_lo[lr] : __builtin_nanf("");   // NaN: never a candidate
     const float hi = act ? st_hi[lr] : __builtin_inff();
     uint2* wdst = (g == 0 && act) ? reinterpret_cast<uint2*>(bbase + (int64_t)row * b_st) : nullptr;
-    const int writer = (4 * wave + g + lr) & 63;
-    uint32_t* pk = pkey + lr * (kPrivCap * 64) + writer;    // slot i at pk[64 * i]
-    uint16_t* pp = ppos + lr * (kPrivCap * 64) + writer;
+    const int writer = (wave + 16 * g + lr) & 63;
+    uint32_t* pk = pkey + lr * (kPrivSlots * 64) + writer;  // slot i at pk[64 * i]
+    uint16_t* pp = ppos + lr * (kPrivSlots * 64) + writer;
     int pc = 0;                                   // candidates of this writer, spilled ones included
     int nsure = 0;
     // One tile's scores -> sure bits in w2, candidates into the lists.  The
@@ -605,11 +633,12 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
           const float s = sc[e];
           const bool le = s <= hi;
           w2[u >> 1] |= le ? 0u : (1u << (16 * (u & 1) + 4 * g + e));   // NaN ranks above every number
-          if (le && s >= lo) {
-            pk[64 * pc] = __float_as_uint(s);
-            pp[64 * pc] = (uint16_t)(col0 + e);
-            ++pc;
-          }
+          // every slot is stored, a non-candidate into the trash slot: no branch
+          const bool cand = le && s >= lo;
+          const int slot = cand ? pc : kPrivCap;
+          pk[64 * slot] = __float_as_uint(s);
+          pp[64 * slot] = (uint16_t)(col0 + e);
+          pc += cand ? 1 : 0;
         }
       } else {
 #pragma unroll
@@ -711,8 +740,8 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
       if (sa.force_fallback || n_ovf > kOvfCap || need < 0 || n_all < need) {
         if (lane == 0) { st_mode[rl] = kFailed; st_any[1] = 1; }
       } else if (need > 0) {
-        const uint32_t* rk = pkey + rl * (kPrivCap * 64) + lane;
-        const uint16_t* rp = ppos + rl * (kPrivCap * 64) + lane;
+        const uint32_t* rk = pkey + rl * (kPrivSlots * 64) + lane;
+        const uint16_t* rp = ppos + rl * (kPrivSlots * 64) + lane;
         const uint32_t* xk = okey + rl * kOvfCap;
         const uint16_t* xp = opos + rl * kOvfCap;
         // f(key, index) for each of the row's candidates held by this lane
@@ -720,18 +749,24 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
           for (int i = 0; i < np; ++i) f(rk[64 * i] & 0x7fffffffu, (int)rp[64 * i]);
           for (int i = lane; i < n_ovf; i += 64) f(xk[i] & 0x7fffffffu, (int)xp[i]);
         };
-        // theta = the need-th largest candidate key, MSB-first over the bits on
-        // which the candidates differ, 8-bit digits counted in LDS.
-        uint32_t kor = 0u, kand = ~0u;
-        each([&](uint32_t kk, int) { kor |= kk; kand &= kk; });
+        // theta = the need-th largest candidate key.  Radix select MSB-first on
+        // key - kmin over the bits of the candidates' key range kmax - kmin,
+        // 8-bit digits counted in LDS: the first digit splits the actual range
+        // of the candidates into 256 bins of about equal width.  A digit whose
+        // keys are all still needed ends the search: theta is then its least key
+        // and every key equal to it is taken.
+        uint32_t kmin = ~0u, kmax = 0u;
+        each([&](uint32_t kk, int) { kmin = min(kmin, kk); kmax = max(kmax, kk); });
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-          kor |= (uint32_t)__shfl_xor((int)kor, o, 64);
-          kand &= (uint32_t)__shfl_xor((int)kand, o, 64);
+          kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
+          kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
         }
-        const uint32_t diff = kor ^ kand;
-        int rem = diff ? 32 - __builtin_clz(diff) : 0;       // low bits still open
-        uint32_t prefix = rem >= 32 ? 0u : (kand & (~0u << rem));
+        auto each_rel = [&](auto&& f) { each([&](uint32_t kk, int ix) { f(kk - kmin, ix); }); };
+        const uint32_t range = kmax - kmin;
+        int rem = range ? 32 - __builtin_clz(range) : 0;     // low bits still open
+        uint32_t prefix = 0u;
+        bool all_ties = false;
         uint32_t* rh = sh_rh[wave];
         while (rem > 0) {
           const int nb = rem < 8 ? rem : 8, shift = rem - nb;
@@ -739,7 +774,7 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
 #pragma unroll
           for (int i = 0; i < 4; ++i) rh[4 * lane + i] = 0u;
           wave_lds_sync();
-          each([&](uint32_t kk, int) {
+          each_rel([&](uint32_t kk, int) {
             if ((kk & hmask) == prefix) atomicAdd(&rh[(kk >> shift) & ((1u << nb) - 1u)], 1u);
           });
           wave_lds_sync();
@@ -748,22 +783,35 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
           for (int i = 0; i < 4; ++i) { cb[i] = (int)rh[4 * lane + i]; vsum += cb[i]; }
           const int suf = wave_suffix(vsum, lane);            // keys in digits >= 4 * lane
           // the highest digit d with count(digits >= d) >= need
-          int dsel = -1, above = 0, c = suf;
+          int dsel = -1, above = 0, cnt = 0, c = suf;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            if (c >= need) { dsel = 4 * lane + i; above = c - cb[i]; }
+            if (c >= need) { dsel = 4 * lane + i; above = c - cb[i]; cnt = cb[i]; }
             c -= cb[i];
           }
           const int d = wave_max(dsel);
           need -= __shfl(above, d >> 2, 64);
+          const int cnt_d = __shfl(cnt, d >> 2, 64);
           prefix |= (uint32_t)d << shift;
           rem = shift;
-        }
-        const uint32_t theta = prefix;
-        int ties = 0;
-        each([&](uint32_t kk, int) { ties += kk == theta ? 1 : 0; });
+          if (rem > 0 && cnt_d == need) {
+            const uint32_t fixed = ~0u << rem;
+            uint32_t least = ~0u;
+            each_rel([&](uint32_t kk, int) { if ((kk & fixed) == prefix) least = min(least, kk); });
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) ties += __shfl_xor(ties, o, 64);
+            for (int o = 1; o < 64; o <<= 1) least = min(least, (uint32_t)__shfl_xor((int)least, o, 64));
+            prefix = least;
+            all_ties = true;
+            break;
+          }
+        }
+        const uint32_t theta = prefix + kmin;
+        int ties = 0;
+        if (!all_ties) {
+          each([&](uint32_t kk, int) { ties += kk == theta ? 1 : 0; });
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) ties += __shfl_xor(ties, o, 64);
+        }
         uint32_t istar = 0xffffffffu;
         if (ties > need) {       // rare: the need lowest indices among the ties, 9-bit digits
           uint32_t ip = 0u;
