@@ -17,6 +17,10 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Never apply __builtin_bit_cast to one element of a vector (`v[i]` of a
+// u32x4): this compiler reads element 0 for every i -- for a loop over
+// `__builtin_bit_cast(bf16x2, v[i])` it loads a single dword.  Copy the
+// element into a scalar first, or bit-cast whole vectors and arrays.
 
 constexpr float kLog2e = 1.4426950408889634f;
 

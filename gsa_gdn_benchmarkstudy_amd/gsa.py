@@ -296,8 +296,9 @@ class GatedSparseAttention(nn.Module):
          with step 3's producer in its epilogue instead);
       2. gsa_indexer_select -- MFMA indexer fused with the exact top-k,
          writing the selection as a bitmask, and for the gather attention
-         ascending int32 indices with per-row counts (the T x T score matrix
-         is never stored) -- beside the q/k/v/gate GEMM while its grid leaves
+         ascending int32 indices with per-row counts (no score is stored:
+         they are recomputed pass by pass and the candidates near each row's
+         threshold stay in LDS) -- beside the q/k/v/gate GEMM while its grid leaves
          CUs free, before it while RoPE(k) and V^T fit the last-level cache,
          else beside the producer; the dense attention's lane masks
          (gsa_dense_lane_masks) follow on the second stream (with the
