@@ -30,10 +30,11 @@ def test_profiled_traffic_lines():
     idx = bench.profiled_traffic("gsa_indexer_select", "c3")
     gather = bench.profiled_traffic("gsa_sparse_attn", "c3")
     # each kernel's HBM bytes per launch at c3, from FETCH_SIZE/WRITE_SIZE: the dense
-    # kernel streams K and V^T tiles (128 MiB) through L2 many times, the indexer
-    # writes and reads back its 537 MB of score tiles, the gather kernel misses L2
-    # on most of its 258 GB of gathered rows
+    # kernel streams K and V^T tiles (128 MiB) through L2 many times; the indexer
+    # reads q_I, k_I, w (10 MiB) and writes the 32 MiB bitmask, storing no score
+    # (a stored causal score matrix alone would be 537 MB); the gather kernel misses
+    # L2 on most of its 258 GB of gathered rows
     assert dense is not None and 0.5e9 < dense < 5e9
-    assert idx is not None and 1.07e9 < idx < 2e9
+    assert idx is not None and 0.044e9 < idx < 0.537e9
     assert gather is not None and 1e11 < gather < 3e11
     assert bench.profiled_traffic("gsa_dense_attn", "c9") is None
