@@ -176,6 +176,43 @@ def test_indexer_select_all_ties_overflow_path(dev, T, k, forced):
         assert sets[t] == set(range(min(t + 1, k)))
 
 
+@pytest.mark.parametrize("forced", [False, True])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_indexer_select_nonfinite_and_extreme_inputs(dev, dtype, forced):
+    """Planted non-finite and extreme inputs: a key with a NaN component (NaN
+    scores in every later row, which rank above every number), a key with an
+    infinite component (logits of +-inf), keys scaled so far that the sigmoid
+    sum's common denominator overflows (the per-head form runs), and a query row
+    whose gate weight is NaN (a whole row of NaN scores: ties, lowest indices
+    win).  The fused selection equals score kernel + selector and the oracle's
+    selector on those scores, on both selection paths."""
+    B, T, k = 1, 1000, 100
+    _log(f"indexer_select non-finite dtype={dtype} forced_fallback={forced}")
+    buf, q, k_, w, bias = _indexer_inputs(B, T, dtype, seed=31, pad=4)
+    buf[0, 200, 256 + 3] = float("nan")           # key 200: NaN dots
+    buf[0, 350, 256 + 7] = float("inf")           # key 350: +-inf dots
+    buf[0, 500:520, 256:320] *= 1e4               # keys 500..519: |logit| in the thousands
+    buf[0, 700, 320 + 1] = float("nan")           # row 700: sigmoid(w) NaN
+    bd = buf.to(dev)
+    qd = bd[..., :256].view(B, T, 4, 64)
+    kd, wd, bias_d = bd[..., 256:320], bd[..., 320:324], bias.to(dev)
+    with _select_mode(forced):
+        fb, fi, fc = _abi.indexer_select(qd, kd, wd, bias_d, 0.125, k)
+    s = _abi.indexer_scores(qd, kd, wd, bias_d, 0.125)
+    sc = s.cpu()
+    assert torch.isnan(sc[0, 300, 200]) and torch.isnan(sc[0, 700, :701]).all()
+    ui, uc, _ = _abi.topk_select(s, k, _abi.ORDER_INDEX_ASC)
+    assert torch.equal(fc.cpu(), uc.cpu())
+    assert torch.equal(fi.cpu(), ui.cpu())
+    assert torch.equal(fb.cpu(), _abi.selection_mask(ui, T, count=uc).cpu())
+    oi, oc = orc.select_ascending(sc, k)
+    assert torch.equal(ui.cpu(), oi) and torch.equal(uc.cpu(), oc)
+    # NaN ranks first: every row past key 200 selects it (but row 700, whose scores
+    # are all NaN: there the lowest indices win)
+    assert all(200 in set(fi[0, t, :fc[0, t]].tolist()) for t in range(201, T) if t != 700)
+    assert fi[0, 700].tolist() == list(range(k))
+
+
 def test_indexer_select_equals_scores_then_topk_T16384(dev):
     """T=16384, k=2048 on synthetic projections: the fused selection (sampled band,
     candidates, resolve) is bit-identical to the full score matrix followed by the
