@@ -239,14 +239,16 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 //           quantile (hypergeometric), z = 5;
 //   main    exact scores of every tile: s > hi (or NaN) is a sure winner and
 //           goes straight into the row's 64-bit mask word (one store per
-//           quad); lo <= s <= hi is a candidate, appended as (key, index)
-//           to the row's list in LDS; below lo is dropped;
+//           quad); lo <= s <= hi is a candidate, kept as (score bits, key
+//           index) in the LDS list of the lane that computed it, or in the
+//           row's overflow list once that one is full; below lo is dropped;
 //   resolve a row is proven exact when n_sure <= k <= n_sure + n_cand (the
 //           k best in (score desc, index asc) order are then the sure ones and
 //           the first k - n_sure candidates in that order): one wave per row
 //           radix-selects the threshold key among the candidates with 8-bit
-//           digit histograms, breaks ties at it by lowest index, and ORs the
-//           winners into the mask;
+//           digit histograms, the first digit spanning the candidates' own
+//           key range, breaks ties at it by lowest index, and ORs the winners
+//           into the mask;
 //   fallback  a row that fails the check (the band missed -- about 6e-7 per
 //           row on independent scores -- its list overflowed, or degenerate
 //           scores put the whole row in the band) is selected by an exact
@@ -258,8 +260,9 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IdxArgs p, int caus
 // counter, which the compiler's waits count in issue order: a wait for a
 // prefetched key tile also waits for any store issued after it on some path
 // that the compiler cannot count.  So the tile loops issue a fixed number of
-// vector memory instructions per tile -- key loads two tiles ahead,
-// unconditional (clamped to the last tile), and one unconditional mask-word
+// vector memory instructions per tile -- the next tile's key loads, issued
+// before this tile's are consumed, unconditional (clamped to the last tile)
+// and into the other of two register buffers, and one unconditional mask-word
 // store per quad (lanes with nothing to write store to a sink slot) --
 // and the candidate lists, the only data-dependent writes, live in LDS.
 // ---------------------------------------------------------------------------
@@ -270,17 +273,17 @@ constexpr int kGroupThreads = 64 * kGroupWaves;
 // Candidate lists.  Each row has 64 writers -- its four lanes in each of the
 // 16 waves -- and every writer a private list of kPrivCap slots; a writer
 // whose list is full spills into the row's overflow list (kOvfCap slots,
-// filled through an atomic counter).
+// filled through an atomic counter).  A row holds 64 * 12 + 384 = 1152
+// candidates at most; a row with more takes the fallback.
 constexpr int kPrivCap = 12;
 constexpr int kPrivSlots = kPrivCap + 1;          // + one trash slot per writer (stores of non-candidates)
 constexpr int kOvfCap = 384;
 constexpr int kPrivWords = 16 * kPrivSlots * 64; // private slots of the 16 rows: [row][slot][writer]
 constexpr int kKeyWords = kPrivWords + 16 * kOvfCap;
-constexpr int kRowCap = 64 * kPrivCap + kOvfCap; // candidates per row at most (1152)
 constexpr float kBandZ = 5.f;             // band half-width in standard deviations of the sample rank
 constexpr int kFbStride = 512;            // fallback digit histograms: 16 rows x 512 words
 // LDS words shared by the phases: the sample histograms (16 x kHStride); the
-// candidate keys (private [16][kPrivCap][64] then overflow [16][kOvfCap], u32)
+// candidate keys (private [16][kPrivSlots][64] then overflow [16][kOvfCap], u32)
 // and positions (the same two arrays in u16); the fallback's digit
 // histograms (16 x kFbStride).
 constexpr int kPoolWords = kKeyWords + kKeyWords / 2;
