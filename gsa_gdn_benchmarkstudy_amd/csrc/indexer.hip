@@ -273,11 +273,13 @@ constexpr int kGroupThreads = 64 * kGroupWaves;
 // Candidate lists.  Each row has 64 writers -- its four lanes in each of the
 // 16 waves -- and every writer a private list of kPrivCap slots; a writer
 // whose list is full spills into the row's overflow list (kOvfCap slots,
-// filled through an atomic counter).  A row holds 64 * 12 + 384 = 1152
-// candidates at most; a row with more takes the fallback.
+// filled through an atomic counter).  A row holds 64 * 12 + 640 = 1408
+// candidates at most (the band of a row of 16384 keys at k = 4096 holds about
+// 1000); a row with more takes the fallback.  The lists fill the LDS a block
+// may use: 138 KiB of pool + 19 KiB of fixed arrays.
 constexpr int kPrivCap = 12;
 constexpr int kPrivSlots = kPrivCap + 1;          // + one trash slot per writer (stores of non-candidates)
-constexpr int kOvfCap = 384;
+constexpr int kOvfCap = 640;
 constexpr int kPrivWords = 16 * kPrivSlots * 64; // private slots of the 16 rows: [row][slot][writer]
 constexpr int kKeyWords = kPrivWords + 16 * kOvfCap;
 constexpr float kBandZ = 5.f;             // band half-width in standard deviations of the sample rank
