@@ -250,10 +250,13 @@ constexpr size_t kDenseLds = (size_t)2 * (kKU + kVU) * 16;   // two K slots, the
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // Value of lane l^32 combined with the own value: permlane32_swap of (v, v)
-// leaves {v[l], v[l^32]} in the two results on every lane.
+// leaves {v[l], v[l^32]} in the two results on every lane.  max_halves takes
+// values that are never NaN (maxima seeded with -inf), so a compare-select
+// is enough (fmaxf would first quiet both operands).
 __device__ __forceinline__ float max_halves(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return a > b ? a : b;
 }
 __device__ __forceinline__ float sum_halves(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -410,7 +413,10 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-  float m = -__builtin_inff(), l = 0.f;
+  // softmax state of the lane's row: reference m (log2 domain), m + kLazy,
+  // -m (0 while m = -inf), and the running sum l
+  float m = -__builtin_inff(), mlz = -__builtin_inff(), nm = 0.f, l = 0.f;
+  const bf16x2 ones2 = __builtin_bit_cast(bf16x2, 0x3f803f80u);   // (1, 1)
 
   // this wave's lane masks: group kDW*qb + w (wave index uniform for scalar loads)
   const uint64_t* lmw = lm + ((int64_t)b * p.G + kDW * qb + wu) * p.NT * 32;
@@ -433,8 +439,13 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
   };
   // masked online-softmax step over one half: p = 2^(s*scale*log2e - m)
   // against a per-row reference m that only moves when the row max exceeds
-  // it by more than kLazy (p <= 2^kLazy; O and l are rescaled rarely; out =
-  // O / l does not depend on m).  Returns P as two B operands of O^T.
+  // it by more than kLazy (p <= 2^kLazy; out = O / l does not depend on m).
+  // A move is rare, so its bookkeeping -- alpha = 2^(m_old - m_new), l *=
+  // alpha, the new m, m + kLazy and -m -- runs in a branch that the wave
+  // takes only when one of its rows moves; the caller then rescales O by
+  // alpha before this half's PV.  l sums the bf16 P values that the PV
+  // product uses, one dot2 per pair.  Returns P as two B operands of O^T and
+  // whether any row of the wave moved (uniform).
   auto softmax_half = [&](const floatx16& acc, const uint64_t* lmt, int c, uint32_t (&pk)[2][4],
                           float& alpha) -> bool {
     float sv[16];
@@ -446,21 +457,25 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
       mx = fmaxf(mx, sv[r]);
     }
     mx = max_halves(mx) * p.scale_l2;
-    const bool bump = mx > m + kLazy || (m == -__builtin_inff() && mx != -__builtin_inff());
-    const float mref = bump ? mx : m;
-    alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
-    const float msafe = mref == -__builtin_inff() ? 0.f : mref;
-    float lsum = 0.f;
+    // mx > m + kLazy; while m = -inf: any selected key (mx is never NaN)
+    const bool moved = ballot64(mx > mlz) != 0;
+    if (moved) {
+      const bool bump = mx > mlz;
+      alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
+      l *= alpha;
+      m = bump ? mx : m;
+      mlz = m + kLazy;
+      nm = m == -__builtin_inff() ? 0.f : -m;
+    }
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], p.scale_l2, -msafe));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r + 1], p.scale_l2, -msafe));
-      pk[r >> 3][(r & 7) >> 1] = pack_bf16(p0, p1);
-      lsum += p0 + p1;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], p.scale_l2, nm));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r + 1], p.scale_l2, nm));
+      const uint32_t w = pack_bf16(p0, p1);
+      pk[r >> 3][(r & 7) >> 1] = w;
+      l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones2, l, false);
     }
-    l = l * alpha + lsum;
-    m = mref;
-    return bump;
+    return moved;
   };
   auto rescale = [&](float alpha) {
 #pragma unroll
@@ -517,9 +532,9 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
     const bool bump0 = softmax_half(sc[P][0], lmt, 0, pk0, alpha0);
     sc[1 - P][1] = s_half(1 - P, 1);
     const bool bump1 = softmax_half(sc[P][1], lmt, 1, pk1, alpha1);
-    if (ballot64(bump0)) rescale(alpha0);
+    if (bump0) rescale(alpha0);
     pv_half(P, 0, pk0);
-    if (ballot64(bump1)) rescale(alpha1);
+    if (bump1) rescale(alpha1);
     pv_half(P, 1, pk1);
     lmt += 32;
   };
