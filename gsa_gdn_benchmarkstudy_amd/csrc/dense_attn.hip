@@ -437,18 +437,18 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
     for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[s], qop[s], acc, 0, 0, 0);
     return acc;
   };
-  // masked online-softmax step over one half: p = 2^(s*scale*log2e - m)
-  // against a per-row reference m that only moves when the row max exceeds
-  // it by more than kLazy (p <= 2^kLazy; out = O / l does not depend on m).
-  // A move is rare, so its bookkeeping -- alpha = 2^(m_old - m_new), l *=
-  // alpha, the new m, m + kLazy and -m -- runs in a branch that the wave
-  // takes only when one of its rows moves; the caller then rescales O by
-  // alpha before this half's PV.  l sums the bf16 P values that the PV
-  // product uses, one dot2 per pair.  Returns P as two B operands of O^T and
-  // whether any row of the wave moved (uniform).
-  auto softmax_half = [&](const floatx16& acc, const uint64_t* lmt, int c, uint32_t (&pk)[2][4],
-                          float& alpha) -> bool {
-    float sv[16];
+  // Masked online softmax, one step per 64-key tile: p = 2^(s*scale*log2e -
+  // m) against a per-row reference m that only moves when the tile's row max
+  // exceeds it by more than kLazy (p <= 2^kLazy; out = O / l does not depend
+  // on m).  mask_half keeps the selected scores of one 32-key half (the others
+  // -inf) and returns their max; both halves are masked before the tile's one
+  // reference decision, so their lane-mask loads and the S^T MFMAs of the next
+  // tile share one stretch of code.  A move is rare: its bookkeeping --
+  // alpha = 2^(m_old - m_new), O and l times alpha, the new m, m + kLazy and
+  // -m -- runs in a branch the wave takes only when one of its rows moves.
+  // exp_half turns a half's scores into P (two B operands of O^T) and adds
+  // the bf16 values that the PV product uses to l, one dot2 per pair.
+  auto mask_half = [&](const floatx16& acc, const uint64_t* lmt, int c, float (&sv)[16]) -> float {
     float mx = -__builtin_inff();
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -456,17 +456,9 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
       sv[r] = sel ? acc[r] : -__builtin_inff();
       mx = fmaxf(mx, sv[r]);
     }
-    mx = max_halves(mx) * p.scale_l2;
-    // mx > m + kLazy; while m = -inf: any selected key (mx is never NaN)
-    const bool moved = ballot64(mx > mlz) != 0;
-    if (moved) {
-      const bool bump = mx > mlz;
-      alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
-      l *= alpha;
-      m = bump ? mx : m;
-      mlz = m + kLazy;
-      nm = m == -__builtin_inff() ? 0.f : -m;
-    }
+    return mx;                                      // never NaN: the max is seeded with -inf
+  };
+  auto exp_half = [&](const float (&sv)[16], uint32_t (&pk)[2][4]) {
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
       const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], p.scale_l2, nm));
@@ -475,7 +467,6 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
       pk[r >> 3][(r & 7) >> 1] = w;
       l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones2, l, false);
     }
-    return moved;
   };
   auto rescale = [&](float alpha) {
 #pragma unroll
@@ -526,15 +517,26 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
     ksrc += kstep;
     vsrc += kDK * 2;
 
-    uint32_t pk0[2][4], pk1[2][4];
-    float alpha0, alpha1;
+    float sv0[16], sv1[16];
     sc[1 - P][0] = s_half(1 - P, 0);               // S^T(kt+1) || softmax(kt); stale on the last tile, unused
-    const bool bump0 = softmax_half(sc[P][0], lmt, 0, pk0, alpha0);
+    const float mx0 = mask_half(sc[P][0], lmt, 0, sv0);
     sc[1 - P][1] = s_half(1 - P, 1);
-    const bool bump1 = softmax_half(sc[P][1], lmt, 1, pk1, alpha1);
-    if (bump0) rescale(alpha0);
+    const float mx1 = mask_half(sc[P][1], lmt, 1, sv1);
+    const float mx = max_halves(mx1 > mx0 ? mx1 : mx0) * p.scale_l2;
+    // mx > m + kLazy; while m = -inf: any selected key
+    if (ballot64(mx > mlz)) {
+      const bool bump = mx > mlz;
+      const float alpha = bump ? __builtin_amdgcn_exp2f(m - mx) : 1.f;   // m = -inf -> 0
+      rescale(alpha);
+      l *= alpha;
+      m = bump ? mx : m;
+      mlz = m + kLazy;
+      nm = m == -__builtin_inff() ? 0.f : -m;
+    }
+    uint32_t pk0[2][4], pk1[2][4];
+    exp_half(sv0, pk0);
     pv_half(P, 0, pk0);
-    if (bump1) rescale(alpha1);
+    exp_half(sv1, pk1);
     pv_half(P, 1, pk1);
     lmt += 32;
   };
