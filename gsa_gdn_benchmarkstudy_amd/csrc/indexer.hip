@@ -34,6 +34,9 @@ template <> struct Mfma<uint16_t> {
   __device__ static Op load(const uint16_t* rowp, int off, int s, int g) {
     return *reinterpret_cast<const bf16x8*>(rowp + off + s * 32 + g * 8);
   }
+  // the same element group from a byte address (row start + group_bytes(g))
+  __device__ static uint32_t group_bytes(int g) { return (uint32_t)g * 16u; }
+  __device__ static Op load_at(const char* p, int s) { return *reinterpret_cast<const bf16x8*>(p + s * 64); }
   __device__ static floatx4 mma(Op a, Op b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
@@ -45,6 +48,8 @@ template <> struct Mfma<float> {
   __device__ static Op load(const float* rowp, int off, int s, int g) {
     return rowp[off + s * 4 + g];
   }
+  __device__ static uint32_t group_bytes(int g) { return (uint32_t)g * 4u; }
+  __device__ static Op load_at(const char* p, int s) { return *reinterpret_cast<const float*>(p + s * 16); }
   __device__ static floatx4 mma(Op a, Op b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
@@ -68,8 +73,9 @@ struct RowGroup {
   float c01, c23;                                 // a0 + a1, a2 + a3
   float bias_l2[kHi];                             // -bias[h] * log2(e)
   float scale_l2;                                 // -scale * log2(e)
-  const T* kbase;                                 // k_idx of this batch
-  int64_t k_st;
+  const char* kbase;                              // k_idx of this batch
+  int64_t kst_bytes;                              // its row stride in bytes
+  uint32_t koff;                                  // the lane's byte offset in a key tile
 
   __device__ void init(const IdxArgs& p, int b, int r0, int lane) {
     const int g = lane >> 4, lr = lane & 15;
@@ -90,19 +96,24 @@ struct RowGroup {
     }
     c01 = a[0] + a[1];
     c23 = a[2] + a[3];
-    kbase = static_cast<const T*>(p.k) + b * p.k_sb;
-    k_st = p.k_st;
+    kbase = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + b * p.k_sb);
+    kst_bytes = p.k_st * (int64_t)sizeof(T);
+    koff = (uint32_t)((lane & 15) * kst_bytes) + Mfma<T>::group_bytes(g);
 #pragma unroll
     for (int h = 0; h < kHi; ++h) bias_l2[h] = -p.bias[h] * kLog2e;
     scale_l2 = p.scale_l2;
   }
 
-  // A operand of key tile [j0, j0+16): key j0 + lane%16, clamped to a valid row.
+  // A operand of key tile [j0, j0+16): key j0 + lane%16, clamped to a valid
+  // row.  The tile's base is uniform (scalar arithmetic) and each lane adds
+  // its 32-bit offset; only a tile that reaches past row T-1 (the last one)
+  // computes clamped offsets.  (The host keeps 16 rows of k below 2^31 bytes.)
   __device__ void load_keys(int j0, int T_, int lane, typename Mfma<T>::Op (&kb)[Mfma<T>::kSteps]) const {
-    const int j = min(j0 + (lane & 15), T_ - 1);
-    const T* krp = kbase + (int64_t)j * k_st;
+    const char* tb = kbase + (int64_t)j0 * kst_bytes;
+    uint32_t off = koff;
+    if (j0 + 16 > T_) off = (uint32_t)(min(lane & 15, T_ - 1 - j0) * kst_bytes) + Mfma<T>::group_bytes(lane >> 4);
 #pragma unroll
-    for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = Mfma<T>::load(krp, 0, s, lane >> 4);
+    for (int s = 0; s < Mfma<T>::kSteps; ++s) kb[s] = Mfma<T>::load_at(tb + off, s);
   }
 
   __device__ void mma(const typename Mfma<T>::Op (&kb)[Mfma<T>::kSteps], floatx4 (&acc)[kHi]) const {
@@ -1076,6 +1087,7 @@ static int check_indexer_args(const void* q, int64_t q_sb, int64_t q_st, const v
   if (B < 1 || T < 1 || Hi != gsa::kHi || di != gsa::kDi) return GSA_ERR_SHAPE;
   if (!vec_ok(q, q_sb, q_st, dtype) || !vec_ok(k, k_sb, k_st, dtype)) return GSA_ERR_ALIGN;
   if (!aligned(w, dtype_size(dtype)) || !aligned(bias, 4)) return GSA_ERR_ALIGN;
+  if (k_st < 0 || k_st * dtype_size(dtype) * 16 >= (int64_t)1 << 31) return GSA_ERR_SHAPE;   // 32-bit tile offsets
   return GSA_OK;
 }
 

@@ -75,6 +75,9 @@ def test_indexer_scores_validation(lib):
     assert _scores(lib, T=0) == 2
     assert _scores(lib, q=MIS) == 4
     assert _scores(lib, qst=260) == 4        # row stride not a multiple of 8 bf16
+    # key tiles are addressed by 32-bit offsets: 16 rows of k must span < 2 GiB
+    assert _scores(lib, kst=1 << 26) == 2
+    assert _scores(lib, kst=-64) == 2
 
 
 NWS_T32 = 2 * 512    # indexer-select workspace at B=1, T=32: two 16-row groups' store slots
@@ -104,6 +107,7 @@ def test_indexer_select_validation(lib):
     assert _select(lib, nws=NWS_T32 - 1) == 2     # workspace too small
     assert _select(lib, ws=P + 8) == 4
     assert _select(lib, T=65537, k_eff=8, bst=2 * 1025, nws=1 << 30) == 2   # past the fused selector's largest T
+    assert _select(lib, kst=1 << 26) == 2         # 16 key rows past 2 GiB (32-bit tile offsets)
     # the candidate lists live in LDS: per 16-row group the workspace holds
     # only 64 8-byte store slots -- linear in T, 2 MiB at T = 65536
     assert lib.gsa_indexer_select_workspace_bytes(1, 32) == NWS_T32 == 2 * 512
