@@ -11,7 +11,10 @@
  *  - Tensors are [B, T, ...] with the innermost dimensions (heads, then
  *    elements) contiguous; each tensor is described by its pointer and its
  *    batch and row strides, in elements.  Strided views into one fused
- *    projection output are therefore accepted without copies.
+ *    projection output are therefore accepted without copies.  The indexer
+ *    entry points address 16 rows of k_idx with 32-bit offsets: they reject
+ *    (GSA_ERR_SHAPE) a negative k_idx row stride or one whose 16 rows span
+ *    2 GiB or more.
  *  - dtype is GSA_DTYPE_BF16 or GSA_DTYPE_F32 for every floating tensor of a
  *    call (indices and counts are int32, masks uint8, scores and bias fp32).
  *  - Ownership: the caller owns every buffer.  The library never allocates,
