@@ -460,6 +460,42 @@ def test_dense_attention_vs_oracle_and_gather(dev, B, T, H, k):
         assert rel < 5e-3
 
 
+@pytest.mark.parametrize("slope", [12.0, -12.0])
+def test_dense_attention_moving_softmax_reference(dev, slope):
+    """Logits that climb (or fall) by about `slope` log2 units per 64-key tile.
+    Climbing, every tile moves every row's lazy softmax reference, so O and l
+    are rescaled by about 2^-12 over and over while they hold earlier keys'
+    weight; falling, the first tile's reference holds and later weights fade
+    towards 0.  Against a float64 oracle: a rescale that is skipped, applied
+    twice or applied after a half's PV product shows as an O(1) error."""
+    _log(f"dense_attn moving reference slope={slope}")
+    B, T, H, k = 1, 640, 2, 160
+    g = torch.Generator().manual_seed(17)
+    scale = 128 ** -0.5
+    a = 4.0                                           # query component along dim 0
+    gamma = slope / (64 * scale * 1.4426950408889634) / a   # key j carries gamma * j along dim 0
+    q = 0.1 * torch.randn(B, T, H, 128, generator=g)
+    q[..., 0] = a
+    kk = 0.1 * torch.randn(B, T, H, 128, generator=g)
+    kk[..., 0] = gamma * torch.arange(T, dtype=torch.float32).view(1, T, 1)
+    q, kk = q.to(torch.bfloat16), kk.to(torch.bfloat16)
+    v = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    s = torch.rand(B, T, T, generator=g).masked_fill(
+        torch.triu(torch.ones(T, T, dtype=torch.bool), 1), float("-inf"))
+    ia, cnt = orc.select_ascending(s, k)
+    vt = torch.zeros(B, H, 128, _abi.vt_len(T), dtype=torch.bfloat16, device=dev)
+    vt[..., :T] = v.to(dev).permute(0, 2, 3, 1)
+    bits = _abi.selection_mask(ia.to(dev), T, count=cnt.to(dev))
+    out = _abi.dense_attn(q.to(dev), kk.to(dev), vt, bits, scale).cpu()
+    mask = torch.arange(k)[None, None, :] < cnt[..., None]
+    ref = orc.sparse_attention(q.double(), kk.double(), v.double(), ia, mask, scale)
+    diff = (out.double() - ref).abs()
+    _log(f"  max|diff| {diff.max().item():.2e}")
+    # the bound of test_dense_attention_vs_oracle_and_gather: P rounded to bf16
+    # (2^-8 * max|v|) and one bf16 output rounding
+    assert torch.all(diff <= ref.abs() * 2 ** -7 + 2 ** -8 * v.abs().max().item() + 1e-6)
+
+
 def test_dense_attention_noncausal_selection(dev):
     """A selection with keys after the query (non-causal) is honoured with causal=False."""
     B, T, H, k = 1, 128, 2, 8
