@@ -45,9 +45,11 @@ struct ProVtArgs {
 
 // Block `blk` of the producer (one (b, h, 64-key tile)); sV: kDK * kKS elements of LDS.
 __device__ __forceinline__ void prologue_vt_block(const ProVtArgs& p, int blk, uint16_t* sV) {
-  const int kt = blk % p.ntiles;
-  const int bh = blk / p.ntiles;
-  const int h = bh % p.H, b = bh / p.H;
+  // heads fastest: the blocks that run side by side read one key tile's
+  // rows of every head (4 KiB of contiguous k, v and vg per key)
+  const int h = blk % p.H;
+  const int kt = (blk / p.H) % p.ntiles;
+  const int b = blk / (p.H * p.ntiles);
   const int j0 = kt * kDK;
   const int tid = threadIdx.x, li = tid & 15;
 #pragma unroll
@@ -216,12 +218,10 @@ __global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p,
 // are then contiguous keys, and its V^T operand is one 16-byte read.
 //
 // Tiles are pipelined: S^T of tile t+1 is computed, one 32-key half at a
-// time, while the softmax of tile t runs half by half, then O^T += V^T(t)
-// P^T(t), so MFMA and VALU work of one wave overlap.  Each 32-key half is one
-// online-softmax step with the lazy reference (below), with its own 16
-// lane-mask words.  (One step per 64-key tile, with all 32 words loaded at
-// once, ran 1.5 % faster at T=16384 and 5.5 % slower at T=65536, where the
-// masks no longer stay in the last-level cache.)
+// time, while tile t's scores are masked half by half (each half with its
+// own 16 lane-mask words), then the tile's one online-softmax decision with
+// the lazy reference (below), then O^T += V^T(t) P^T(t) half by half, so
+// MFMA and VALU work of one wave overlap.
 // ---------------------------------------------------------------------------
 struct DenseArgs {
   const uint16_t* q; int64_t q_sb, q_st;
