@@ -310,10 +310,14 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
   const int wu = __builtin_amdgcn_readfirstlane(w);
   const int i32 = lane & 31, h = lane >> 5;
   // heaviest query blocks first
-  const int nbh = p.B * p.H;
-  const int qb = p.nqb - 1 - (int)(blockIdx.x / nbh);
-  const int rem = blockIdx.x % nbh;
-  const int b = rem / p.H, hd = rem % p.H;
+  // Block order: batch by batch (the blocks in flight then share one
+  // sequence's K and V^T, which stays in the last-level cache), within a
+  // sequence the heaviest query blocks first, heads fastest.
+  const int per_b = p.nqb * p.H;
+  const int b = (int)(blockIdx.x / per_b);
+  const int r2 = (int)(blockIdx.x % per_b);
+  const int qb = p.nqb - 1 - r2 / p.H;
+  const int hd = r2 % p.H;
   const int q0 = qb * kDQ;
   const int qrow = q0 + 32 * w + i32;
   const int qr = min(qrow, p.T - 1);
