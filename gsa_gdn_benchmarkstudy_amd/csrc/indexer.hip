@@ -760,9 +760,19 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
         const uint16_t* rp = ppos + rl * (kPrivSlots * 64) + lane;
         const uint32_t* xk = okey + rl * kOvfCap;
         const uint16_t* xp = opos + rl * kOvfCap;
+        // The lane's private list -- writer `lane`'s, np <= kPrivCap entries --
+        // is read from LDS once into registers (keys in ck, two 16-bit indices
+        // per cp word); the overflow slots lane, lane + 64, ... stay in LDS.
+        uint32_t ck[kPrivCap], cp[kPrivCap / 2];
+#pragma unroll
+        for (int i = 0; i < kPrivCap; ++i) ck[i] = rk[64 * i] & 0x7fffffffu;
+#pragma unroll
+        for (int i = 0; i < kPrivCap / 2; ++i) cp[i] = (uint32_t)rp[128 * i] | ((uint32_t)rp[128 * i + 64] << 16);
         // f(key, index) for each of the row's candidates held by this lane
         auto each = [&](auto&& f) {
-          for (int i = 0; i < np; ++i) f(rk[64 * i] & 0x7fffffffu, (int)rp[64 * i]);
+#pragma unroll
+          for (int i = 0; i < kPrivCap; ++i)
+            if (i < np) f(ck[i], (int)((cp[i >> 1] >> (16 * (i & 1))) & 0xffffu));
           for (int i = lane; i < n_ovf; i += 64) f(xk[i] & 0x7fffffffu, (int)xp[i]);
         };
         // theta = the need-th largest candidate key.  Radix select MSB-first on
