@@ -302,6 +302,9 @@ constexpr int kFbStride = 512;            // fallback digit histograms: 16 rows 
 constexpr int kPoolWords = kKeyWords + kKeyWords / 2;
 static_assert(16 * kHStride <= kPoolWords && 16 * kFbStride <= kPoolWords, "LDS pool too small");
 constexpr size_t kPoolBytes = (size_t)kPoolWords * 4;
+// The kernel's static arrays take about 19 KiB beside the pool; a block may
+// use 160 KiB of LDS.
+static_assert(kPoolBytes + 20 * 1024 <= 160 * 1024, "select LDS budget exceeded");
 constexpr size_t kSinkBytes = 64 * 8;     // per 16-row group: the mask-word store slots of non-writing lanes
 // A candidate's key index is kept in 16 bits (and the 16-bit sample counts
 // hold at most 16 * ceil(T/64) keys per row).
