@@ -131,10 +131,47 @@ __global__ __launch_bounds__(256) void selection_mask_kernel(
 // selection bit of row 32g+i and key 64kt + 32c + 16(r/8) + 8h + r%8 -- the
 // key that accumulator r of lane (h, i) holds in the S^T MFMA output of half
 // c (see the key order below).  One wave per (b, g, 4 consecutive tiles):
-// lane (h, i) reads row 32g+i's four 64-bit words, then one ballot per slot
-// transposes them; lanes 0..31 write each tile's 256 contiguous bytes.
+// lane (h, i) reads row 32g+i's four 64-bit words and keeps keys 32h..32h+31
+// of each; a 32x32 bit transpose in each half of the wave turns the rows into
+// key columns (lane k: bit i = row 32g+i's bit of key k), and slot lane s
+// takes its two columns; lanes 0..31 write each tile's 256 contiguous bytes.
 // ---------------------------------------------------------------------------
 constexpr int kLmTiles = 4;
+
+// 32x32 bit transpose inside each 32-lane half of the wave: on entry lane i
+// of a half holds row i (bit j = element (i, j)), on exit lane j holds
+// column j (bit i = element (i, j)).  Stage b (16, 8, 4, 2, 1) swaps the
+// off-diagonal b x b blocks of every 2b x 2b block between lanes i and i ^ b:
+// the lane with bit b clear keeps the low b bits of each 2b-bit group and
+// takes its partner's low ones, shifted up by b, into the high b; the other
+// lane keeps the high b bits and takes its partner's high ones shifted down.
+// Both shifts are one right rotation of the partner's word (by 32 - b or by
+// b: the bits that wrap around land in the part the lane keeps), so a stage
+// is a lane swizzle, a rotate and a bit select with per-lane constants.
+struct BitTranspose {
+  uint32_t keep[5], rot[5];   // per stage: bits the lane keeps, right rotation of the partner's word
+  __device__ explicit BitTranspose(int lane) {
+    constexpr uint32_t kLow[5] = {0x0000ffffu, 0x00ff00ffu, 0x0f0f0f0fu, 0x33333333u, 0x55555555u};
+#pragma unroll
+    for (int st = 0; st < 5; ++st) {
+      const int b = 16 >> st;
+      const bool up = (lane & b) != 0;
+      keep[st] = up ? ~kLow[st] : kLow[st];
+      rot[st] = up ? (uint32_t)b : (uint32_t)(32 - b);
+    }
+  }
+  // ds_swizzle bit mode (and 0x1f, or 0, xor B): lane ^ B within its 32-lane half
+  template <int St>
+  __device__ __forceinline__ uint32_t stage(uint32_t x) const {
+    constexpr int B = 16 >> St;
+    const uint32_t y = (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, (B << 10) | 0x1f);
+    const uint32_t sh = __builtin_amdgcn_alignbit(y, y, rot[St]);
+    return (x & keep[St]) | (sh & ~keep[St]);
+  }
+  __device__ __forceinline__ uint32_t operator()(uint32_t x) const {
+    return stage<4>(stage<3>(stage<2>(stage<1>(stage<0>(x)))));
+  }
+};
 
 struct LaneMaskArgs {
   const uint32_t* bits; int64_t b_sb, b_st;
@@ -160,25 +197,23 @@ __device__ __forceinline__ void lane_mask_block(const LaneMaskArgs& a, int blk) 
   const uint64_t* src = reinterpret_cast<const uint64_t*>(bits + b * b_sb + (int64_t)min(row, T - 1) * b_st) + kt0;
 #pragma unroll
   for (int u = 0; u < kLmTiles; ++u) words[u] = (row < T && kt0 + u < NT) ? src[u] : 0ull;
+  // slot s = 16c + r (lane s < 32) holds key k0 = 32c + 16(r/8) + r%8 in its
+  // low 32 bits (lanes h = 0) and key k0 + 8 in its high 32 bits (h = 1)
+  const int s = lane & 31, k0 = 32 * (s >> 4) + 16 * ((s >> 3) & 1) + (s & 7);
+  const BitTranspose transpose(lane);
 #pragma unroll
   for (int u = 0; u < kLmTiles; ++u) {
     if (kt0 + u >= NT) break;
-    const uint64_t word = words[u] >> (8 * h);
-    int lo = 0, hi = 0;                      // slot s's mask lands in lane s
+    uint64_t out = 0;
     // A tile no row of the group selects from (every tile past the group's
     // diagonal, for a causal selection) has all-zero masks: no transpose.
     if (ballot64(words[u] != 0ull)) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint64_t m = ballot64((word >> (32 * c + 16 * (r >> 3) + (r & 7))) & 1ull);
-          const bool mine = __builtin_amdgcn_inverse_ballot_w64(1ull << (16 * c + r));   // lane == slot
-          lo = mine ? (int)(uint32_t)m : lo;
-          hi = mine ? (int)(uint32_t)(m >> 32) : hi;
-        }
+      const uint32_t col = transpose((uint32_t)(words[u] >> (32 * h)));   // key `lane`'s column
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * k0, (int)col);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (k0 + 8), (int)col);
+      out = ((uint64_t)hi << 32) | lo;
     }
-    if (lane < 32) lm[((int64_t)bg * NT + kt0 + u) * 32 + lane] = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+    if (lane < 32) lm[((int64_t)bg * NT + kt0 + u) * 32 + lane] = out;
   }
 }
 

@@ -538,6 +538,47 @@ def test_dense_lane_masks_then_attention_equals_one_call(dev):
     assert torch.equal(one.cpu(), two.cpu())
 
 
+def _lane_masks_expected(bits, T, Tkv):
+    """The dense attention's lane-mask words, stated from the bitmask alone:
+    word [b, g, kt, s] (s = 16c + r) has bit 32h + i set iff row 32g + i (< T)
+    selects key 64kt + 32c + 16(r // 8) + 8h + r % 8, the key that accumulator
+    r of lane (h, i) holds in half c of the S^T MFMA output."""
+    B = bits.shape[0]
+    NT = (Tkv + 63) // 64
+    G = (T + 255) // 256 * 8
+    w = bits.cpu().numpy().view(np.uint32).astype(np.uint64)
+    w64 = w[..., 0::2] | (w[..., 1::2] << np.uint64(32))                  # [B, T, NT]
+    rows = np.zeros((B, G * 32, NT), np.uint64)
+    rows[:, :T] = w64
+    rows = rows.reshape(B, G, 32, NT)
+    s = np.arange(32)
+    out = np.zeros((B, G, NT, 32), np.uint64)
+    for h in range(2):
+        key = (32 * (s // 16) + 16 * ((s % 16) // 8) + 8 * h + s % 8).astype(np.uint64)
+        bit = (rows[..., None] >> key) & np.uint64(1)                      # [B, G, i, NT, s]
+        shift = (32 * h + np.arange(32)).astype(np.uint64)[None, None, :, None, None]
+        out |= np.bitwise_or.reduce(bit << shift, axis=2)
+    return out
+
+
+@pytest.mark.parametrize("B,T,Tkv,density", [(2, 300, 300, 0.5), (1, 777, 1000, 0.1), (1, 64, 64, 0.9),
+                                             (3, 520, 130, 0.03)])
+def test_dense_lane_masks_layout(dev, B, T, Tkv, density):
+    """gsa_dense_lane_masks against the layout stated from the bitmask, on a random
+    (not causal: every word populated) selection, ragged T and T != Tkv."""
+    _log(f"lane masks layout B={B} T={T} Tkv={Tkv} density={density}")
+    g = torch.Generator().manual_seed(T + Tkv)
+    sel = torch.rand(B, T, (Tkv + 63) // 64 * 64, generator=g) < density
+    sel[..., Tkv:] = False
+    words = (sel.view(B, T, -1, 32).to(torch.int64) << torch.arange(32)).sum(-1)
+    bits = words.to(torch.int32).contiguous().to(dev)
+    ws = _abi.dense_lane_masks(bits, Tkv)
+    torch.cuda.synchronize()
+    want = _lane_masks_expected(bits, T, Tkv)
+    got = ws[:want.size * 8].cpu().numpy().view(np.uint64).reshape(want.shape)
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("B,T,H", [(1, 100, 2), (2, 256, 4), (1, 700, 3)])
 def test_prologue_vt_lane_masks_equals_two_launches(dev, B, T, H):
     """gsa_prologue_vt_lane_masks (producer and lane masks in one launch, blocks
