@@ -880,10 +880,10 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
         // bitmap in this row's private-key region of LDS (kBitmapWords words,
         // free: the lists are in ck/cp now), then each nonzero word of the
         // bitmap is ORed into the stored word by one read-modify-write: one
-        // wave owns the row here, and the main pass's stores reached L2
-        // before the barrier (agent-scope loads do not take a stale copy from
-        // the CU's cache).  Longer rows take several chunks.  (Global atomics
-        // per winner instead: c3 0.333 ms, B=4 T=8192 0.371 ms.)
+        // wave owns the row here, and the main pass's stores, made by this
+        // workgroup and complete before the barrier (vmcnt(0)), are visible
+        // to its loads after it.  Longer rows take several chunks.  (Global
+        // atomics per winner instead: c3 0.333 ms, B=4 T=8192 0.371 ms.)
         constexpr int kBitmapWords = kPrivSlots * 64;
         uint32_t* brow = bbase + (int64_t)(r0 + rl) * b_st;
         uint32_t* bm = pkey + rl * kBitmapWords;
@@ -902,7 +902,7 @@ __global__ __launch_bounds__(kGroupThreads) void indexer_select_kernel(IdxArgs p
             const uint32_t v = bm[j];
             if (v) {
               uint32_t* pw = brow + c0 + j;
-              *pw = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) | v;
+              *pw = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) | v;
             }
           }
           wave_lds_sync();                               // the bitmap's reads before the next chunk's zeros
