@@ -266,6 +266,9 @@ def main():
         views = model.project(x)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # one untimed call first: the GPU runs it while the host records e0 and
+        # enqueues the timed calls, so no host time falls between the events
+        model.select(views, T, indices=not model.uses_dense(dtype))
         e0.record()
         n_idx = 5
         for _ in range(n_idx):
