@@ -153,6 +153,25 @@ def test_indexer_select_equals_scores_then_topk(dev, dtype, B, T, k, forced):
     assert torch.equal(ui.cpu(), oi) and torch.equal(uc.cpu(), oc)
 
 
+def test_indexer_select_long_rows_equal_scores_then_topk(dev):
+    """Rows of more than 832 causal mask words (keys past 26624): the resolve ORs
+    their band winners into the stored words in two bitmap chunks.  Fused select
+    against the score kernel + selector on the same inputs, bit for bit (the
+    unfused path is pinned to the oracle's selector at smaller T)."""
+    B, T, k = 1, 27000, 2048
+    _log(f"indexer_select long rows B={B} T={T} k={k}")
+    buf, q, k_, w, bias = _indexer_inputs(B, T, torch.bfloat16, seed=27, pad=4)
+    bd = buf.to(dev)
+    qd = bd[..., :256].view(B, T, 4, 64)
+    kd, wd, bias_d = bd[..., 256:320], bd[..., 320:324], bias.to(dev)
+    fb, fi, fc = _abi.indexer_select(qd, kd, wd, bias_d, 0.125, k)
+    s = _abi.indexer_scores(qd, kd, wd, bias_d, 0.125)
+    ui, uc, _ = _abi.topk_select(s, k, _abi.ORDER_INDEX_ASC)
+    del s
+    assert torch.equal(fc, uc) and torch.equal(fi, ui)
+    assert torch.equal(fb, _abi.selection_mask(ui, T, count=uc))
+
+
 @pytest.mark.parametrize("forced", [False, True])
 @pytest.mark.parametrize("T,k", [(700, 100), (300, 299), (1500, 40), (3000, 1000)])
 def test_indexer_select_all_ties_overflow_path(dev, T, k, forced):
