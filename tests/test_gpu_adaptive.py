@@ -154,6 +154,39 @@ def test_indexer_select_adaptive_vs_oracle(dev, dtype, B, T, k_base, k_min, k_ma
         assert np.array_equal(un[rows[:, 0], rows[:, 1]], exp), f"bitmask k={kv}"
 
 
+def test_indexer_select_adaptive_long_rows(dev):
+    """Variance-based k at T=27000: rows past key 26624 (more than 832 causal mask
+    words) take two LDS bitmap chunks in the resolve.  On sampled rows, each row's
+    variance against float64 and its selection against the oracle's selector at the
+    kernel's own k_t, indices and bitmask bit for bit (k_t itself is checked against
+    the oracle's formula at smaller T)."""
+    B, T, k_base, k_min, k_max = 1, 27000, 2048, 256, 4096
+    _log(f"indexer_select_adaptive long rows B={B} T={T}")
+    buf, bias = _indexer_inputs(B, T, torch.bfloat16, seed=270)
+    bd = buf.to(dev)
+    qd = bd[..., :256].view(B, T, 4, 64)
+    kd, wd, bias_d = bd[..., 256:320], bd[..., 320:324], bias.to(dev)
+    bits, idx, cnt, k_rows, var = _abi.indexer_select_adaptive(qd, kd, wd, bias_d, 0.125, k_base, k_min, k_max)
+    rows = [0, 1, 2047, 4096, 13000] + list(range(26600, 26640)) + list(range(T - 48, T))
+    rsel = torch.tensor(rows, device=dev)
+    S = _abi.indexer_scores(qd, kd, wd, bias_d, 0.125)[0].index_select(0, rsel).cpu()
+    k_rows, var, idx, cnt = k_rows[0].cpu(), var[0].cpu(), idx[0].cpu(), cnt[0].cpu()
+    v64 = _var64(S)
+    vr = var[rows].double().numpy()
+    rel = np.abs(vr - v64) / np.maximum(v64, 1e-12)
+    assert np.all((rel <= 1e-4) | (np.abs(vr - v64) <= 1e-9)), f"var max rel err {rel.max():.2e}"
+    un = _bits_sets(bits[:, rows])[0]
+    for r, t in enumerate(rows):
+        kt = int(k_rows[t])
+        oi, oc = orc.select_ascending(S[r].view(1, 1, T), kt)
+        n = int(oc[0, 0])
+        assert int(cnt[t]) == n and torch.equal(idx[t, :n], oi[0, 0, :n]), f"row {t} k={kt}"
+        exp = np.zeros(un.shape[-1], dtype=np.uint8)
+        exp[oi[0, 0, :n].numpy()] = 1
+        assert np.array_equal(un[r], exp), f"bitmask row {t}"
+    _log(f"  k_t on the sampled rows {int(k_rows[rows].min())}..{int(k_rows[rows].max())}")
+
+
 def test_indexer_select_adaptive_degenerate_scores(dev):
     """Every score equal (q = 0): every variance is 0, so k_t = k_base (clamped)
     everywhere and ties resolve to the lowest indices (the overflow path)."""
