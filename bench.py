@@ -330,7 +330,7 @@ def main():
                                                 "many queries select come from the caches, so this rate "
                                                 "is not an HBM rate and may exceed the HBM peak"}}
     if attn_impl == "dense":
-        qrows = 256                              # query rows per block of gsa_dense_attn
+        qrows = _abi.dense_block_rows(T)         # query rows per block of gsa_dense_attn
         nqb = (T + qrows - 1) // qrows
         dense_flops = 4 * B * H * DH * qrows * 64 * sum(min(qb * qrows + qrows - 1, T - 1) // 64 + 1
                                                          for qb in range(nqb))

@@ -1,5 +1,5 @@
 // Block-dense sparse attention on gfx950 MFMA: every causal key tile is
-// streamed once per 256-row query block and the exact top-k selection is
+// streamed once per query block and the exact top-k selection is
 // applied as a bitmask, so masked-out keys get probability 0.  Same function
 // as the gather kernel (softmax over each row's selected keys), different
 // work: dense MFMA over the causal triangle instead of per-row gathers.
@@ -9,8 +9,8 @@
 // selection bits [B,T,W] uint32, W = 2*ceil(Tkv/64): bit j of row t set iff
 // key j is selected and valid for query t.
 //
-// Per block: one head, 256 query rows, 8 waves of 32 rows, 64-key tiles
-// in LDS.  With v_mfma_f32_32x32x16_bf16 both products are computed
+// Per block: one head, 256 query rows (8 waves of 32 rows; 384 rows in 12
+// waves from 32K keys on), 64-key tiles in LDS.  With v_mfma_f32_32x32x16_bf16 both products are computed
 // transposed,
 //   S^T = K Q^T    (A = K tile from LDS, B = this wave's q, in registers)
 //   O^T = V^T P^T  (A = V^T tile from LDS, B = P in registers)
@@ -23,8 +23,12 @@
 
 namespace gsa {
 
-constexpr int kDW = 8;           // waves per dense-attention block (32 query rows each)
-constexpr int kDQ = 32 * kDW;    // query rows per dense-attention block
+// Waves per dense-attention block (32 query rows each): 8 for keys shorter
+// than kDenseWideTkv, 12 from there on.  The lane-mask layout follows the
+// same rule (its 32-row groups are padded to whole blocks), so producer and
+// consumer agree from (T, Tkv) alone.
+constexpr int kDenseWideTkv = 32768;
+__host__ __device__ constexpr int dense_block_waves(int Tkv) { return Tkv >= kDenseWideTkv ? 12 : 8; }
 constexpr int kDK = 64;          // keys per tile
 constexpr int kKS = 128 + 8;     // LDS row stride of prologue_vt's staging tile (elements)
 
@@ -236,8 +240,8 @@ __global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p,
 // ---------------------------------------------------------------------------
 // Dense masked attention (bf16)
 //
-// Block: kDW = 8 waves = 256 query rows of one head (wave w: rows 32w ..
-// 32w+31), two waves per SIMD.  K and V^T tiles reach LDS by direct
+// Block: W waves = 32W query rows of one head (wave w: rows 32w .. 32w+31):
+// 8 waves (two per SIMD) or 12 (three per SIMD), by dense_block_waves.  K and V^T tiles reach LDS by direct
 // global->LDS loads (16 B per lane; one instruction fills 1 KiB,
 // lane-linear), K tiles and V^T tiles each through a pair of slots, in padded
 // layouts (unit = 16 B = 8 bf16):
@@ -252,11 +256,12 @@ __global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p,
 // holds key 16(r/8) + 8h + r%8.  A lane's 8 P values of each 16-key k-step
 // are then contiguous keys, and its V^T operand is one 16-byte read.
 //
-// Tiles are pipelined: S^T of tile t+1 is computed, one 32-key half at a
-// time, while tile t's scores are masked half by half (each half with its
-// own 16 lane-mask words), then the tile's one online-softmax decision with
-// the lazy reference (below), then O^T += V^T(t) P^T(t) half by half, so
-// MFMA and VALU work of one wave overlap.
+// Tiles are pipelined (8 waves): S^T of tile t+1 is computed, one 32-key
+// half at a time, while tile t's scores are masked half by half (each half
+// with its own 16 lane-mask words), then the tile's one online-softmax
+// decision with the lazy reference (below), then O^T += V^T(t) P^T(t) half by
+// half, so MFMA and VALU work of one wave overlap.  12-wave blocks compute
+// S^T(t) itself in that place (one S accumulator pair per wave).
 // ---------------------------------------------------------------------------
 struct DenseArgs {
   const uint16_t* q; int64_t q_sb, q_st;
@@ -278,8 +283,6 @@ constexpr int kKU = kDK * kKRow;       // 1088 units: K tile
 constexpr int kVU = 128 * kVRow;       // 1152 units: V^T tile
 constexpr int kDmaK = kKU / 64;        // 17 load instructions fill a K tile
 constexpr int kDmaV = kVU / 64;        // 18 fill a V^T tile
-constexpr int kDmaKW = (kDmaK + kDW - 1) / kDW;   // K instructions per wave (wave w: i = kDW*n + w < 17)
-constexpr int kDmaVW = (kDmaV + kDW - 1) / kDW;   // V^T instructions per wave
 constexpr size_t kDenseLds = (size_t)2 * (kKU + kVU) * 16;   // two K slots, then two V^T slots
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -326,20 +329,34 @@ __device__ __forceinline__ int swap_bits23(int i) { return (i & ~12) | ((i & 4) 
 
 template <int N> struct Int { static constexpr int value = N; };
 
-// Pipeline of one block (kDW waves = kDQ query rows of one head), tile t = 64
+// Pipeline of one block (W waves = 32W query rows of one head), tile t = 64
 // keys.  K tiles and V^T tiles stream through separate pairs of LDS slots
-// (tile t in slot t&1).  Iteration t, after one barrier:
+// (tile t in slot t&1).  With PP (ping-pong S), iteration t, after one
+// barrier:
 //   loads  K(t+2) into K slot t&1 (S(t) was computed last iteration) and
 //          V^T(t+1) into V slot (t+1)&1 (PV(t-1) is done);
 //   MFMA   S^T(t+1) from K slot (t+1)&1, interleaved with the softmax of
 //          S(t) (VALU), then O^T += V^T(t) P^T(t) from V slot t&1.
-// So the S product of the next tile overlaps the softmax of this one.  Every
-// load is issued one iteration before the barrier that publishes it; the
-// loop is unrolled by two so that slot offsets are constants.
+// So the S product of the next tile overlaps the softmax of this one, within
+// the wave, at the cost of a second S accumulator pair (64 VGPRs).  Without
+// PP, iteration t loads K(t+1) and V^T(t+1) into slots (t+1)&1 and computes
+// S^T(t), its softmax and PV(t) from slots t&1: one S pair, so 12-wave blocks
+// (three waves per SIMD) fit the register file, and the overlap of MFMA and
+// VALU work comes from the other waves of the SIMD instead.  8 waves with PP
+// is the faster form up to 16K keys, 12 without PP beyond (fewer tile loads
+// per query row: at 65536 keys 17.1 -> 15.9 ms, K and V^T no longer fit the
+// last-level cache).  Every load is issued one iteration before the barrier
+// that publishes it; the loop is unrolled by two so that slot offsets are
+// constants.
 // lm is a separate restrict argument: nothing in this kernel writes it, and
 // alias analysis can see that, so its uniform reads stay scalar loads.
-__global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs p, const uint64_t* __restrict__ lm) {
+template <int W, bool PP>
+__global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, const uint64_t* __restrict__ lm) {
   extern __shared__ __align__(16) u32x4 dsm[];   // K slots 0, 1 (kKU units each), then V^T slots 0, 1 (kVU)
+  constexpr int kDW = W;                          // waves per block
+  constexpr int kDQ = 32 * W;                     // query rows per block
+  constexpr int kDmaKW = (kDmaK + kDW - 1) / kDW;   // K instructions per wave (wave w: i = kDW*n + w < 17)
+  constexpr int kDmaVW = (kDmaV + kDW - 1) / kDW;   // V^T instructions per wave
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(w);
@@ -406,9 +423,9 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
       if (n + 1 < kDmaVW || n < nvw)
         load_lds16(src, voff[n], vdst + (uint32_t)(slot * kVU * 16 + n * kDW * 1024));
   };
-  // prologue loads: K(0), K(1), V(0)
+  // prologue loads: K(0), K(1) (ping-pong only), V(0)
   issue_k(kbase, 0, nkt == 1);
-  if (nkt > 1) issue_k(kbase + kstep, 1, nkt == 2);
+  if (PP && nkt > 1) issue_k(kbase + kstep, 1, nkt == 2);
   issue_v(vtb, 0);
 
   // ---- q: B operand of S^T; lane supplies d = 16s + 8h .. +7 of its row ----
@@ -547,41 +564,21 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
   // loads and any such wait would drain them.
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
-  // S^T of tile kt in sc[kt & 1]: with the loop unrolled by two, each
-  // iteration writes the other pair, so no accumulator is copied
-  floatx16 sc[2][2];
-  sc[0][0] = s_half(0, 0);
-  sc[0][1] = s_half(0, 1);                          // S^T of tile 0
-
-  const char* ksrc = kbase + 2 * kstep;              // K tile kt+2
   const char* vsrc = vtb + kDK * 2;                  // V^T tile kt+1
   const uint64_t* lmt = lmw;                         // lane masks of tile kt
   // The first half's 16 lane-mask words of a tile are loaded one iteration
   // ahead, after the previous tile's masks are used, so their scalar loads
   // are in flight during the PV products and done at the next barrier (at
-  // T=65536 the masks come from HBM: 18.3 -> 17.0 ms).  The second half's
-  // are loaded where they are used: holding both halves ahead would need 32
-  // more SGPRs and spills 130 of them.
+  // T=65536 the masks come from HBM; with 8-wave blocks 18.3 -> 17.0 ms).
+  // The second half's are loaded where they are used: holding both halves
+  // ahead would need 32 more SGPRs and spills 130 of them.
   uint64_t mw0[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) mw0[r] = lmw[r];
-  // one iteration; P = kt & 1
-  auto step = [&](int kt, auto par) {
-    constexpr int P = decltype(par)::value;
-    // this wave's loads of K(kt+1) and V^T(kt) (issued last iteration) are
-    // done and its LDS reads have returned; the barrier publishes every
-    // wave's loads and frees K slot P and V slot 1-P
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kt + 2 < nkt) issue_k(ksrc, P, kt + 3 == nkt);
-    if (kt + 1 < nkt) issue_v(vsrc, 1 - P);
-    ksrc += kstep;
-    vsrc += kDK * 2;
-
-    float sv0[16], sv1[16];
-    sc[1 - P][0] = s_half(1 - P, 0);               // S^T(kt+1) || softmax(kt); stale on the last tile, unused
-    const float mx0 = mask_half_r(sc[P][0], mw0, sv0);
-    sc[1 - P][1] = s_half(1 - P, 1);
-    const float mx1 = mask_half(sc[P][1], lmt, 1, sv1);
+  // Tile kt once both halves are masked (scores sv0, sv1, maxima mx0, mx1):
+  // the softmax decision, P, O^T += V^T(kt) P^T(kt) from V slot vs, and the
+  // next tile's first-half mask words.
+  auto softmax_pv = [&](int kt, int vs, float mx0, float mx1, const float (&sv0)[16], const float (&sv1)[16]) {
     const float mx = max_halves(mx1 > mx0 ? mx1 : mx0) * p.scale_l2;
     // mx > m + kLazy; while m = -inf: any selected key
     if (ballot64(mx > mlz)) {
@@ -595,21 +592,78 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
     }
     uint32_t pk0[2][4], pk1[2][4];
     exp_half(sv0, pk0);
-    pv_half(P, 0, pk0);
+    pv_half(vs, 0, pk0);
     exp_half(sv1, pk1);
-    pv_half(P, 1, pk1);
+    pv_half(vs, 1, pk1);
     if (kt + 1 < nkt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mw0[r] = lmt[32 + r];
     }
     lmt += 32;
   };
-  int kt = 0;
-  for (; kt + 1 < nkt; kt += 2) {
-    step(kt, Int<0>{});
-    step(kt + 1, Int<1>{});
+
+  if constexpr (PP) {
+    // S^T of tile kt in sc[kt & 1]: with the loop unrolled by two, each
+    // iteration writes the other pair, so no accumulator is copied
+    floatx16 sc[2][2];
+    sc[0][0] = s_half(0, 0);
+    sc[0][1] = s_half(0, 1);                        // S^T of tile 0
+    const char* ksrc = kbase + 2 * kstep;            // K tile kt+2
+    // one iteration; P = kt & 1
+    auto step = [&](int kt, auto par) {
+      constexpr int P = decltype(par)::value;
+      // this wave's loads of K(kt+1) and V^T(kt) (issued last iteration) are
+      // done and its LDS reads have returned; the barrier publishes every
+      // wave's loads and frees K slot P and V slot 1-P
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (kt + 2 < nkt) issue_k(ksrc, P, kt + 3 == nkt);
+      if (kt + 1 < nkt) issue_v(vsrc, 1 - P);
+      ksrc += kstep;
+      vsrc += kDK * 2;
+
+      float sv0[16], sv1[16];
+      sc[1 - P][0] = s_half(1 - P, 0);             // S^T(kt+1) || softmax(kt); stale on the last tile, unused
+      const float mx0 = mask_half_r(sc[P][0], mw0, sv0);
+      sc[1 - P][1] = s_half(1 - P, 1);
+      const float mx1 = mask_half(sc[P][1], lmt, 1, sv1);
+      softmax_pv(kt, P, mx0, mx1, sv0, sv1);
+    };
+    int t = 0;
+    for (; t + 1 < nkt; t += 2) {
+      step(t, Int<0>{});
+      step(t + 1, Int<1>{});
+    }
+    if (t < nkt) step(t, Int<0>{});
+  } else {
+    const char* ksrc = kbase + kstep;                // K tile kt+1
+    // one iteration; P = kt & 1
+    auto step = [&](int kt, auto par) {
+      constexpr int P = decltype(par)::value;
+      // this wave's loads of K(kt) and V^T(kt) (issued last iteration) are
+      // done and its LDS reads have returned; the barrier publishes every
+      // wave's loads and frees slots 1-P (tile kt-1) for tile kt+1
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (kt + 1 < nkt) {
+        issue_k(ksrc, 1 - P, kt + 2 == nkt);
+        issue_v(vsrc, 1 - P);
+      }
+      ksrc += kstep;
+      vsrc += kDK * 2;
+
+      float sv0[16], sv1[16];
+      const floatx16 s0 = s_half(P, 0);
+      const float mx0 = mask_half_r(s0, mw0, sv0);
+      const floatx16 s1 = s_half(P, 1);
+      const float mx1 = mask_half(s1, lmt, 1, sv1);
+      softmax_pv(kt, P, mx0, mx1, sv0, sv1);
+    };
+    int t = 0;
+    for (; t + 1 < nkt; t += 2) {
+      step(t, Int<0>{});
+      step(t + 1, Int<1>{});
+    }
+    if (t < nkt) step(t, Int<0>{});
   }
-  if (kt < nkt) step(kt, Int<0>{});
 
   // ---- epilogue: normalise, bf16, optional output gate ----
   l = sum_halves(l);
@@ -647,10 +701,11 @@ __global__ __launch_bounds__(64 * kDW, 8 / kDW) void dense_attn_kernel(DenseArgs
 // ---------------------------------------------------------------------------
 using namespace gsa_host;
 
-// Per device: the dense kernel's LDS limit has been raised.  (A benign race:
-// concurrent first calls both set the same attribute.)
+// Per device and dense kernel (8 waves, 12 waves): its LDS limit has been
+// raised.  (A benign race: concurrent first calls both set the same
+// attribute.)
 static constexpr int kMaxDevices = 64;
-static bool g_dense_lds_set[kMaxDevices] = {};
+static bool g_dense_lds_set[kMaxDevices][2] = {};
 
 namespace {
 int prologue_vt_checks(const void* k, int64_t k_sb, int64_t k_st, const void* v, int64_t v_sb, int64_t v_st,
@@ -706,12 +761,20 @@ extern "C" int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st
   return launch_status();
 }
 
+namespace {
+// 32-row lane-mask groups of T query rows: whole blocks of the dense kernel
+// that runs for Tkv keys (8 groups per block, 12 from 32K keys on).
+int64_t dense_groups(int T, int Tkv) {
+  const int w = gsa::dense_block_waves(Tkv);
+  return (int64_t)((T + 32 * w - 1) / (32 * w)) * w;
+}
+}  // namespace
+
 // Lane masks: 32 per (batch, 32-row group, 64-key tile); the groups are
-// counted over whole 256-row query blocks.
+// counted over whole query blocks of the dense kernel.
 extern "C" size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv) {
   if (B < 1 || T < 1 || Tkv < 1) return 0;
-  const size_t groups = (size_t)((T + gsa::kDQ - 1) / gsa::kDQ) * (gsa::kDQ / 32);
-  return (size_t)B * groups * ((Tkv + 63) / 64) * 32 * sizeof(uint64_t);
+  return (size_t)B * (size_t)dense_groups(T, Tkv) * ((Tkv + 63) / 64) * 32 * sizeof(uint64_t);
 }
 
 namespace {
@@ -723,9 +786,7 @@ int lane_mask_checks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, in
   const int NT = (Tkv + 63) / 64;
   if (b_st < 2 * NT || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
   if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
-  const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
-  const int G = nqb * (gsa::kDQ / 32);
-  if ((int64_t)B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
+  if ((int64_t)B * dense_groups(T, Tkv) * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
   if (!aligned(bits, 8) || (b_sb % 2) || (b_st % 2) || !aligned(ws, 8)) return GSA_ERR_ALIGN;
   return GSA_OK;
 }
@@ -733,8 +794,7 @@ int lane_mask_checks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, in
 gsa::LaneMaskArgs lane_mask_args(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv,
                                   void* ws) {
   const int NT = (Tkv + 63) / 64;
-  const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
-  const int G = nqb * (gsa::kDQ / 32);
+  const int G = (int)dense_groups(T, Tkv);
   const int nwaves = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
   return gsa::LaneMaskArgs{bits, b_sb, b_st, T, G, NT, nwaves, static_cast<uint64_t*>(ws)};
 }
@@ -801,9 +861,10 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
   // per-lane load offsets within a tile are 32-bit byte offsets
   if (k_st > (1 << 24) || (int64_t)ldv > (1 << 23)) return GSA_ERR_SHAPE;
-  const int nqb = (T + gsa::kDQ - 1) / gsa::kDQ;
-  const int G = nqb * (gsa::kDQ / 32);    // 32-row groups, padded to whole blocks
-  if ((int64_t)B * H * nqb > 0x7fffffffLL || (int64_t)B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
+  const int W = gsa::dense_block_waves(Tkv);   // waves per block: 32W query rows
+  const int nqb = (T + 32 * W - 1) / (32 * W);
+  const int64_t G = dense_groups(T, Tkv);      // 32-row groups, padded to whole blocks
+  if ((int64_t)B * H * nqb > 0x7fffffffLL || B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
   if (!vec_ok(q, q_sb, q_st, dtype) || !vec_ok(k, k_sb, k_st, dtype) || !vec_ok(vt, vt_sb, vt_sh, dtype) ||
       !vec_ok(out, out_sb, out_st, dtype) || !aligned(ws, 8))
     return GSA_ERR_ALIGN;
@@ -822,19 +883,25 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   }
   flags &= ~GSA_ATTN_MASKS_READY;
   gsa::DenseArgs a{static_cast<const uint16_t*>(q), q_sb, q_st, static_cast<const uint16_t*>(k), k_sb, k_st,
-                   static_cast<const uint16_t*>(vt), vt_sb, vt_sh, ldv, G, NT,
+                   static_cast<const uint16_t*>(vt), vt_sb, vt_sh, ldv, (int)G, NT,
                    static_cast<const uint16_t*>(og), o_sb, o_st, static_cast<const uint16_t*>(cos),
                    static_cast<const uint16_t*>(sin), cs_st, static_cast<uint16_t*>(out), out_sb, out_st,
                    B, T, Tkv, H, nqb, scale * gsa::kLog2e, flags | (causal ? gsa::kDenseCausal : 0)};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return GSA_ERR_SHAPE;
-  if (!g_dense_lds_set[dev]) {   // more than the default 64 KiB of LDS per block
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gsa::dense_attn_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsa::kDenseLds);
+  const bool wide = W == 12;
+  const void* fn = wide ? reinterpret_cast<const void*>(gsa::dense_attn_kernel<12, false>)
+                        : reinterpret_cast<const void*>(gsa::dense_attn_kernel<8, true>);
+  if (!g_dense_lds_set[dev][wide]) {   // more than the default 64 KiB of LDS per block
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsa::kDenseLds);
     if (e != hipSuccess) return -static_cast<int>(e);
-    g_dense_lds_set[dev] = true;
+    g_dense_lds_set[dev][wide] = true;
   }
-  hipLaunchKernelGGL(gsa::dense_attn_kernel, dim3(B * H * nqb), dim3(64 * gsa::kDW), gsa::kDenseLds, s, a,
-                     static_cast<const uint64_t*>(lm));
+  if (wide)
+    hipLaunchKernelGGL((gsa::dense_attn_kernel<12, false>), dim3(B * H * nqb), dim3(64 * 12), gsa::kDenseLds, s,
+                       a, static_cast<const uint64_t*>(lm));
+  else
+    hipLaunchKernelGGL((gsa::dense_attn_kernel<8, true>), dim3(B * H * nqb), dim3(64 * 8), gsa::kDenseLds, s, a,
+                       static_cast<const uint64_t*>(lm));
   return launch_status();
 }

@@ -533,6 +533,75 @@ def test_dense_attention_noncausal_selection(dev):
     assert (torch.linalg.vector_norm(out.double() - ref) / torch.linalg.vector_norm(ref)).item() < 5e-3
 
 
+def _long_keys_case(T, Tkv, H, k, seed, causal, key_limit=None):
+    """q [1,T,H,d], k/v [1,Tkv,H,d] and k selected keys per row: random
+    among the row's causal prefix (causal) or among all keys below key_limit."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, T, H, 128, generator=g).to(torch.bfloat16)
+    kk = torch.randn(1, Tkv, H, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, Tkv, H, 128, generator=g).to(torch.bfloat16)
+    og = torch.randn(1, T, H, 128, generator=g).to(torch.bfloat16)
+    s = torch.rand(1, T, Tkv, generator=g)
+    if causal:
+        s = s.masked_fill(torch.arange(Tkv)[None, None, :] > torch.arange(T)[None, :, None], float("-inf"))
+    if key_limit is not None:
+        s[..., key_limit:] = float("-inf")
+    ia, cnt = orc.select_ascending(s, k)
+    return q, kk, v, og, ia, cnt
+
+
+def _vt_of(v, dev):
+    B, Tkv, H, _ = v.shape
+    vt = torch.zeros(B, H, 128, _abi.vt_len(Tkv), dtype=torch.bfloat16, device=dev)
+    vt[..., :Tkv] = v.to(dev).permute(0, 2, 3, 1)
+    return vt
+
+
+@pytest.mark.parametrize("T,Tkv,H,k,causal", [(800, 33000, 2, 300, False), (800, 33000, 2, 300, True),
+                                              (385, 32768, 1, 64, False)])
+def test_dense_attention_long_keys_vs_oracle(dev, T, Tkv, H, k, causal):
+    """From 32768 keys on gsa_dense_attn runs 12-wave (384-row) blocks: ragged
+    query blocks (T = 2*384 + 32, 384 + 1), a ragged last key tile (33000 =
+    515*64 + 40), causal and non-causal selections, RoPE(q) and the output gate,
+    against the float64 oracle with the bound of the short-key test."""
+    _log(f"dense_attn long keys T={T} Tkv={Tkv} H={H} k={k} causal={causal}")
+    q, kk, v, og, ia, cnt = _long_keys_case(T, Tkv, H, k, seed=T + Tkv, causal=causal)
+    cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
+    bits = _abi.selection_mask(ia.to(dev), Tkv, count=cnt.to(dev))
+    flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
+    out = _abi.dense_attn(q.to(dev), kk.to(dev), _vt_of(v, dev), bits, 128 ** -0.5, og=og.to(dev),
+                          cos=cos.to(dev), sin=sin.to(dev), flags=flags, causal=causal).cpu()
+    qr = orc.apply_rope(q, cos[None, :, None], sin[None, :, None])
+    mask = torch.arange(k)[None, None, :] < cnt[..., None]
+    att = orc.sparse_attention(qr.double(), kk.double(), v.double(), ia, mask, 128 ** -0.5)
+    ref = (att.to(torch.bfloat16) * torch.sigmoid(og)).double()
+    diff = (out.double() - ref).abs()
+    rel = (torch.linalg.vector_norm(out.double() - ref) / torch.linalg.vector_norm(ref)).item()
+    _log(f"  rel-L2 {rel:.2e} max|diff| {diff.max().item():.2e}")
+    assert torch.all(diff <= ref.abs() * 2 ** -6 + 2 ** -8 * v.abs().max().item() + 1e-6)
+    assert rel < 5e-3
+
+
+def test_dense_attention_block_shapes_bit_identical(dev):
+    """The 12-wave kernel (32768 keys) and the 8-wave one (the first 32000 of
+    the same keys) on a selection that only uses keys below 32000: every row
+    runs the same per-wave arithmetic in both (the extra tiles are fully
+    masked and add exact zeros), so the outputs agree bit for bit."""
+    T, H, k = 1000, 2, 256
+    _log(f"dense_attn 12-wave vs 8-wave blocks T={T} H={H} k={k}")
+    assert _abi.dense_block_rows(32768) == 384 and _abi.dense_block_rows(32000) == 256
+    q, kk, v, og, ia, cnt = _long_keys_case(T, 32768, H, k, seed=7, causal=False, key_limit=32000)
+    cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
+    qd, ogd, cosd, sind, iad, cntd = (t.to(dev) for t in (q, og, cos, sin, ia, cnt))
+    flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
+    outs = []
+    for Tkv in (32768, 32000):
+        bits = _abi.selection_mask(iad, Tkv, count=cntd)
+        outs.append(_abi.dense_attn(qd, kk[:, :Tkv].contiguous().to(dev), _vt_of(v[:, :Tkv], dev), bits,
+                                    128 ** -0.5, og=ogd, cos=cosd, sin=sind, flags=flags, causal=False).cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_dense_lane_masks_then_attention_equals_one_call(dev):
     """gsa_dense_lane_masks on another stream, then gsa_dense_attn with
     GSA_ATTN_MASKS_READY: the same output as the one-call path, bit for bit."""
@@ -564,7 +633,8 @@ def _lane_masks_expected(bits, T, Tkv):
     r of lane (h, i) holds in half c of the S^T MFMA output."""
     B = bits.shape[0]
     NT = (Tkv + 63) // 64
-    G = (T + 255) // 256 * 8
+    rows_per_block = _abi.dense_block_rows(Tkv)                          # groups cover whole blocks
+    G = (T + rows_per_block - 1) // rows_per_block * (rows_per_block // 32)
     w = bits.cpu().numpy().view(np.uint32).astype(np.uint64)
     w64 = w[..., 0::2] | (w[..., 1::2] << np.uint64(32))                  # [B, T, NT]
     rows = np.zeros((B, G * 32, NT), np.uint64)
@@ -581,7 +651,9 @@ def _lane_masks_expected(bits, T, Tkv):
 
 
 @pytest.mark.parametrize("B,T,Tkv,density", [(2, 300, 300, 0.5), (1, 777, 1000, 0.1), (1, 64, 64, 0.9),
-                                             (3, 520, 130, 0.03)])
+                                             (3, 520, 130, 0.03),
+                                             # 384-row blocks (12 groups) from 32768 keys on
+                                             (1, 400, 32800, 0.01)])
 def test_dense_lane_masks_layout(dev, B, T, Tkv, density):
     """gsa_dense_lane_masks against the layout stated from the bitmask, on a random
     (not causal: every word populated) selection, ragged T and T != Tkv."""
