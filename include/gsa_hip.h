@@ -311,8 +311,9 @@ int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel
  * gsa_indexer_select or gsa_selection_mask).
  * q, out, og [B,T,H,d]; k [B,Tkv,H,d] (RoPE'd); vt [B,H,d,ldv] as written by
  * gsa_prologue_vt (strides vt_sb, vt_sh per batch and head; rows of ldv).
- * causal != 0: key tiles after a 256-row query block's last row are skipped
- * (the selection must then be causal).  ws: caller-provided device workspace
+ * causal != 0: key tiles after a query block's last row are skipped (the
+ * selection must then be causal; a block holds 256 query rows, 384 when
+ * Tkv >= 32768).  ws: caller-provided device workspace
  * of at least gsa_dense_attn_workspace_bytes(B, T, Tkv) bytes (8-byte
  * aligned), overwritten by each call -- or, with GSA_ATTN_MASKS_READY, the
  * lane masks gsa_dense_lane_masks wrote there for the same bits, B, T and
