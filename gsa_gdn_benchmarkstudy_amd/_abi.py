@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgsa_hip.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -79,10 +79,10 @@ _PROTOS = {
                         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_dense_attn_workspace_bytes": ([_i32, _i32, _i32], ctypes.c_size_t),
     "gsa_proj_packed_bytes": ([_i32, _i32], ctypes.c_size_t),
-    "gsa_dense_lane_masks": ([_vp, _i64, _i64, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
+    "gsa_dense_lane_masks": ([_vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_prologue_vt_lane_masks": ([_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
                                     _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32,
-                                    _vp, _i64, _i64, _i32, _vp, ctypes.c_size_t, _vp], _i32),
+                                    _vp, _i64, _i64, _i32, _i32, _vp, ctypes.c_size_t, _vp], _i32),
     "gsa_proj_pack": ([_vp, _i64, _vp, _i32, _i32, _i32, _vp, _vp, _vp], _i32),
     "gsa_proj_fused": ([_vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64,
                         _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], _i32),
@@ -455,12 +455,14 @@ def dense_block_rows(Tkv: int) -> int:
     return 384 if Tkv >= DENSE_WIDE_TKV else 256
 
 
-def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None, bits=None, Tkv=None, ws=None):
+def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None, bits=None, Tkv=None, ws=None,
+                causal: bool = False):
     """RoPE(k) -> k_out [B,T,H,d] and (v*sigmoid(vg))^T -> vt [B,H,d,ldv] (bf16).
 
     With ``bits`` (the selection bitmask [B,T,W] of keys 0..Tkv-1): the dense
     attention's lane masks are built in the same launch (gsa_prologue_vt_lane_masks)
-    into ``ws`` (allocated when None), returned third: (k_out, vt, ws)."""
+    into ``ws`` (allocated when None), returned third: (k_out, vt, ws).  ``causal``:
+    only the tiles a causal dense_attn reads (the masks then serve causal calls only)."""
     lib = load()
     _need_cuda(k, v, vg, cos, sin, bits, ws)
     B, T, H, d = v.shape
@@ -497,8 +499,8 @@ def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None, bits=Non
     _expect(ws.numel() * ws.element_size() >= nbytes and ws.is_contiguous(), "workspace too small")
     st = lib.gsa_prologue_vt_lane_masks(_ptr(k), *ks, _ptr(v), *_rows(v, HD), _ptr(vg), *_rows(vg, HD), _ptr(cos),
                                         _ptr(sin), cs, B, T, H, d, dtype_code(v.dtype), _ptr(k_out), _ptr(vt),
-                                        ldv, _ptr(bits), bits.stride(0), bits.stride(1), Tkv, _ptr(ws), nbytes,
-                                        _stream(v))
+                                        ldv, _ptr(bits), bits.stride(0), bits.stride(1), Tkv, int(bool(causal)),
+                                        _ptr(ws), nbytes, _stream(v))
     _check(st, "gsa_prologue_vt_lane_masks")
     return k_out, vt, ws
 
@@ -586,9 +588,11 @@ def selection_mask(idx, Tkv: int, count=None, mask=None, out=None):
     return out
 
 
-def dense_lane_masks(bits, Tkv: int, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+def dense_lane_masks(bits, Tkv: int, ws: Optional[torch.Tensor] = None, causal: bool = False) -> torch.Tensor:
     """Lane masks of the dense attention from the selection bitmask [B,T,W] -> the
-    workspace tensor holding them (pass it to dense_attn with masks_ready=True)."""
+    workspace tensor holding them (pass it to dense_attn with masks_ready=True).
+    ``causal``: only the tiles a causal dense_attn reads, up to the last row of each
+    query block (such masks serve causal calls only); otherwise every tile."""
     lib = load()
     _need_cuda(bits, ws)
     B, T, W = bits.shape
@@ -597,8 +601,8 @@ def dense_lane_masks(bits, Tkv: int, ws: Optional[torch.Tensor] = None) -> torch
     if ws is None:
         ws = torch.empty(nbytes, device=bits.device, dtype=torch.uint8)
     _expect(ws.numel() * ws.element_size() >= nbytes and ws.is_contiguous(), "workspace too small")
-    st = lib.gsa_dense_lane_masks(_ptr(bits), bits.stride(0), bits.stride(1), B, T, Tkv, _ptr(ws), nbytes,
-                                  _stream(bits))
+    st = lib.gsa_dense_lane_masks(_ptr(bits), bits.stride(0), bits.stride(1), B, T, Tkv, int(bool(causal)),
+                                  _ptr(ws), nbytes, _stream(bits))
     _check(st, "gsa_dense_lane_masks")
     return ws
 

@@ -180,6 +180,7 @@ struct BitTranspose {
 struct LaneMaskArgs {
   const uint32_t* bits; int64_t b_sb, b_st;
   int T, G, NT, nwaves;
+  int block_rows;   // causal: query rows per attention block (tiles past a block's last row are skipped); else 0
   uint64_t* lm;
 };
 
@@ -197,17 +198,22 @@ __device__ __forceinline__ void lane_mask_block(const LaneMaskArgs& a, int blk) 
   const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
   const int row = 32 * g + i;
   const int kt0 = kq * kLmTiles;
+  // Tiles the attention reads for this group: all of them, or (causal) those
+  // up to the last row of the group's attention block, as its block does.
+  int nt = NT;
+  if (a.block_rows) nt = min(NT, ((32 * g) / a.block_rows + 1) * a.block_rows / kDK);
+  if (kt0 >= nt) return;
   uint64_t words[kLmTiles];
   const uint64_t* src = reinterpret_cast<const uint64_t*>(bits + b * b_sb + (int64_t)min(row, T - 1) * b_st) + kt0;
 #pragma unroll
-  for (int u = 0; u < kLmTiles; ++u) words[u] = (row < T && kt0 + u < NT) ? src[u] : 0ull;
+  for (int u = 0; u < kLmTiles; ++u) words[u] = (row < T && kt0 + u < nt) ? src[u] : 0ull;
   // slot s = 16c + r (lane s < 32) holds key k0 = 32c + 16(r/8) + r%8 in its
   // low 32 bits (lanes h = 0) and key k0 + 8 in its high 32 bits (h = 1)
   const int s = lane & 31, k0 = 32 * (s >> 4) + 16 * ((s >> 3) & 1) + (s & 7);
   const BitTranspose transpose(lane);
 #pragma unroll
   for (int u = 0; u < kLmTiles; ++u) {
-    if (kt0 + u >= NT) break;
+    if (kt0 + u >= nt) break;
     uint64_t out = 0;
     // A tile no row of the group selects from (every tile past the group's
     // diagonal, for a causal selection) has all-zero masks: no transpose.
@@ -792,26 +798,27 @@ int lane_mask_checks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, in
 }
 
 gsa::LaneMaskArgs lane_mask_args(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv,
-                                  void* ws) {
+                                  int causal, void* ws) {
   const int NT = (Tkv + 63) / 64;
   const int G = (int)dense_groups(T, Tkv);
   const int nwaves = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
-  return gsa::LaneMaskArgs{bits, b_sb, b_st, T, G, NT, nwaves, static_cast<uint64_t*>(ws)};
+  const int block_rows = causal ? 32 * gsa::dense_block_waves(Tkv) : 0;
+  return gsa::LaneMaskArgs{bits, b_sb, b_st, T, G, NT, nwaves, block_rows, static_cast<uint64_t*>(ws)};
 }
 
-int launch_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv, void* ws,
-                      hipStream_t s) {
-  const gsa::LaneMaskArgs l = lane_mask_args(bits, b_sb, b_st, B, T, Tkv, ws);
+int launch_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv, int causal,
+                      void* ws, hipStream_t s) {
+  const gsa::LaneMaskArgs l = lane_mask_args(bits, b_sb, b_st, B, T, Tkv, causal, ws);
   hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((l.nwaves + 3) / 4), dim3(256), 0, s, l);
   return launch_status();
 }
 }  // namespace
 
 extern "C" int gsa_dense_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv,
-                                    void* ws, size_t ws_bytes, void* stream) {
+                                    int causal, void* ws, size_t ws_bytes, void* stream) {
   const int st = lane_mask_checks(bits, b_sb, b_st, B, T, Tkv, ws, ws_bytes);
   if (st) return st;
-  return launch_lane_masks(bits, b_sb, b_st, B, T, Tkv, ws, static_cast<hipStream_t>(stream));
+  return launch_lane_masks(bits, b_sb, b_st, B, T, Tkv, causal, ws, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int gsa_prologue_vt_lane_masks(const void* k, int64_t k_sb, int64_t k_st,
@@ -821,7 +828,7 @@ extern "C" int gsa_prologue_vt_lane_masks(const void* k, int64_t k_sb, int64_t k
                                           int B, int T, int H, int d, int dtype,
                                           void* k_out, void* vt, int ldv,
                                           const uint32_t* bits, int64_t b_sb, int64_t b_st, int Tkv,
-                                          void* ws, size_t ws_bytes, void* stream) {
+                                          int causal, void* ws, size_t ws_bytes, void* stream) {
   int st = prologue_vt_checks(k, k_sb, k_st, v, v_sb, v_st, vg, g_sb, g_st, cos, sin, cs_st, B, T, H, d, dtype,
                               k_out, vt, ldv);
   if (st) return st;
@@ -830,7 +837,7 @@ extern "C" int gsa_prologue_vt_lane_masks(const void* k, int64_t k_sb, int64_t k
                    static_cast<const uint16_t*>(vg), g_sb, g_st, static_cast<const uint16_t*>(cos),
                    static_cast<const uint16_t*>(sin), cs_st, static_cast<uint16_t*>(k_out),
                    static_cast<uint16_t*>(vt), T, H, ldv, ldv / 64};
-  const gsa::LaneMaskArgs l = lane_mask_args(bits, b_sb, b_st, B, T, Tkv, ws);
+  const gsa::LaneMaskArgs l = lane_mask_args(bits, b_sb, b_st, B, T, Tkv, causal, ws);
   const int n_pro = B * H * (ldv / 64), n_lm = (l.nwaves + 3) / 4;
   if ((int64_t)n_pro + n_lm > 0x7fffffffLL) return GSA_ERR_SHAPE;
   hipLaunchKernelGGL(gsa::prologue_vt_lane_mask_kernel, dim3(n_pro + n_lm), dim3(256), 0,
@@ -878,7 +885,7 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint64_t* lm = static_cast<uint64_t*>(ws);
   if (!ready) {
-    const int st = launch_lane_masks(bits, b_sb, b_st, B, T, Tkv, ws, s);
+    const int st = launch_lane_masks(bits, b_sb, b_st, B, T, Tkv, causal, ws, s);
     if (st) return st;
   }
   flags &= ~GSA_ATTN_MASKS_READY;

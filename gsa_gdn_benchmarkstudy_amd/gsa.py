@@ -566,7 +566,7 @@ class GatedSparseAttention(nn.Module):
                 lm_stream.wait_stream(cur)
             with torch.cuda.stream(lm_stream):
                 _range_push("gsa_hip/lane_masks")
-                lm_ws = _abi.dense_lane_masks(bits, T)
+                lm_ws = _abi.dense_lane_masks(bits, T, causal=True)   # the layer's attention is causal
                 _range_pop()
         if mode != "producer":
             _range_push("gsa_hip/main_gemm")
@@ -579,7 +579,7 @@ class GatedSparseAttention(nn.Module):
             k_rope, v_gated = views["_k_rope"], views["_vt"]
         elif lm_in_producer:
             k_rope, v_gated, lm_ws = _abi.prologue_vt(views["v"], views["vg"], k=views["k"], cos=cos, sin=sin,
-                                                      bits=bits, Tkv=T)
+                                                      bits=bits, Tkv=T, causal=True)
         elif dense:
             k_rope, v_gated = _abi.prologue_vt(views["v"], views["vg"], k=views["k"], cos=cos, sin=sin)
         else:

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define GSA_ABI_VERSION 1
+#define GSA_ABI_VERSION 2
 
 #define GSA_DTYPE_F32  0
 #define GSA_DTYPE_BF16 1
@@ -316,8 +316,8 @@ int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel
  * Tkv >= 32768).  ws: caller-provided device workspace
  * of at least gsa_dense_attn_workspace_bytes(B, T, Tkv) bytes (8-byte
  * aligned), overwritten by each call -- or, with GSA_ATTN_MASKS_READY, the
- * lane masks gsa_dense_lane_masks wrote there for the same bits, B, T and
- * Tkv (then bits is not read).  bf16 only; d == 128, 1 <= H <= 64.
+ * lane masks gsa_dense_lane_masks wrote there for the same bits, B, T, Tkv
+ * and causal (then bits is not read).  bf16 only; d == 128, 1 <= H <= 64.
  */
 size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
 
@@ -326,10 +326,13 @@ size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
  * per-lane masks of the attention kernel's score slots, into ws (same size
  * and alignment as gsa_dense_attn's workspace).  Lets a caller build them
  * on another stream, beside other work, and pass GSA_ATTN_MASKS_READY.
+ * causal != 0: only the key tiles a causal gsa_dense_attn reads (up to the
+ * last row of each query block) are built; such masks serve causal calls
+ * only.  causal == 0: every tile (serves both).
  * No counterpart in the reference: part of this build's dense attention.
  */
 int gsa_dense_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st,
-                         int B, int T, int Tkv, void* ws, size_t ws_bytes, void* stream);
+                         int B, int T, int Tkv, int causal, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * gsa_prologue_vt (RoPE(k) and v*sigmoid(vg) as V^T: gsa_opt.py:685-697) and
@@ -345,7 +348,7 @@ int gsa_prologue_vt_lane_masks(const void* k, int64_t k_sb, int64_t k_st,
                                int B, int T, int H, int d, int dtype,
                                void* k_out, void* vt, int ldv,
                                const uint32_t* bits, int64_t b_sb, int64_t b_st, int Tkv,
-                               void* ws, size_t ws_bytes, void* stream);
+                               int causal, void* ws, size_t ws_bytes, void* stream);
 
 int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                    const void* k, int64_t k_sb, int64_t k_st,

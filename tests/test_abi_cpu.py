@@ -231,11 +231,11 @@ def test_dense_path_validation(lib):
     assert call(flags=8) == 6                     # unknown flag
     assert call(bst=3) == 4
     lmk = lib.gsa_dense_lane_masks
-    assert lmk(None, 0, 2, 1, 4, 4, P, 8 * 256, None) == 1
-    assert lmk(P, 0, 2, 1, 4, 4, None, 8 * 256, None) == 1
-    assert lmk(P, 0, 2, 1, 4, 4, P, 8 * 256 - 1, None) == 2   # workspace too small
-    assert lmk(P, 0, 1, 1, 4, 4, P, 8 * 256, None) == 2       # row of W words shorter than 2*ceil(Tkv/64)
-    assert lmk(P, 0, 3, 1, 4, 4, P, 8 * 256, None) == 4       # 8-byte aligned rows
+    assert lmk(None, 0, 2, 1, 4, 4, 1, P, 8 * 256, None) == 1
+    assert lmk(P, 0, 2, 1, 4, 4, 1, None, 8 * 256, None) == 1
+    assert lmk(P, 0, 2, 1, 4, 4, 1, P, 8 * 256 - 1, None) == 2   # workspace too small
+    assert lmk(P, 0, 1, 1, 4, 4, 1, P, 8 * 256, None) == 2       # row of W words shorter than 2*ceil(Tkv/64)
+    assert lmk(P, 0, 3, 1, 4, 4, 1, P, 8 * 256, None) == 4       # 8-byte aligned rows
     p = lib.gsa_prologue_vt
     assert p(P, 0, 2048, P, 0, 2048, P, 0, 2048, P, P, 128, 1, 4, 16, 128, 1, P, P, 100, None) == 2   # ldv % 64
     assert p(P, 0, 2048, None, 0, 2048, P, 0, 2048, P, P, 128, 1, 4, 16, 128, 1, P, P, 64, None) == 1

@@ -602,9 +602,11 @@ def test_dense_attention_block_shapes_bit_identical(dev):
     assert torch.equal(outs[0], outs[1])
 
 
-def test_dense_lane_masks_then_attention_equals_one_call(dev):
+@pytest.mark.parametrize("causal_masks", [True, False])
+def test_dense_lane_masks_then_attention_equals_one_call(dev, causal_masks):
     """gsa_dense_lane_masks on another stream, then gsa_dense_attn with
-    GSA_ATTN_MASKS_READY: the same output as the one-call path, bit for bit."""
+    GSA_ATTN_MASKS_READY: the same output as the one-call path, bit for bit,
+    with the causal call's own masks or with masks of every tile."""
     B, T, H, k = 2, 300, 4, 64
     q, kk, v, og, ia, cnt = _dense_case(B, T, H, k, seed=91)
     cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
@@ -618,7 +620,7 @@ def test_dense_lane_masks_then_attention_equals_one_call(dev):
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
-        ws = _abi.dense_lane_masks(bits, T)
+        ws = _abi.dense_lane_masks(bits, T, causal=causal_masks)
     torch.cuda.current_stream(dev).wait_stream(side)
     two = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, og=ogd, cos=cosd, sin=sind, flags=flags,
                           ws=ws, masks_ready=True)
@@ -654,27 +656,40 @@ def _lane_masks_expected(bits, T, Tkv):
                                              (3, 520, 130, 0.03),
                                              # 384-row blocks (12 groups) from 32768 keys on
                                              (1, 400, 32800, 0.01)])
-def test_dense_lane_masks_layout(dev, B, T, Tkv, density):
+@pytest.mark.parametrize("causal", [False, True])
+def test_dense_lane_masks_layout(dev, B, T, Tkv, density, causal):
     """gsa_dense_lane_masks against the layout stated from the bitmask, on a random
-    (not causal: every word populated) selection, ragged T and T != Tkv."""
-    _log(f"lane masks layout B={B} T={T} Tkv={Tkv} density={density}")
+    (not causal: every word populated) selection, ragged T and T != Tkv.  With
+    causal, the tiles up to the last row of each group's query block (the ones a
+    causal attention reads) hold the same words and the rest of the workspace is
+    left as it was."""
+    _log(f"lane masks layout B={B} T={T} Tkv={Tkv} density={density} causal={causal}")
     g = torch.Generator().manual_seed(T + Tkv)
     sel = torch.rand(B, T, (Tkv + 63) // 64 * 64, generator=g) < density
     sel[..., Tkv:] = False
     words = (sel.view(B, T, -1, 32).to(torch.int64) << torch.arange(32)).sum(-1)
     bits = words.to(torch.int32).contiguous().to(dev)
-    ws = _abi.dense_lane_masks(bits, Tkv)
-    torch.cuda.synchronize()
     want = _lane_masks_expected(bits, T, Tkv)
-    got = ws[:want.size * 8].cpu().numpy().view(np.uint64).reshape(want.shape)
-    assert np.array_equal(got, want)
+    ws = torch.full((want.size * 8,), 0xA5, dtype=torch.uint8, device=dev)
+    _abi.dense_lane_masks(bits, Tkv, ws=ws, causal=causal)
+    torch.cuda.synchronize()
+    got = ws.cpu().numpy().view(np.uint64).reshape(want.shape)
+    if not causal:
+        assert np.array_equal(got, want)
+        return
+    rows = _abi.dense_block_rows(Tkv)
+    nt = np.minimum(want.shape[2], ((32 * np.arange(want.shape[1])) // rows + 1) * rows // 64)   # per group
+    read = np.arange(want.shape[2])[None, :] < nt[:, None]                                     # [G, NT]
+    assert np.array_equal(got[:, read], want[:, read])
+    assert np.all(got[:, ~read] == np.uint64(0xA5A5A5A5A5A5A5A5))
 
 
+@pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("B,T,H", [(1, 100, 2), (2, 256, 4), (1, 700, 3)])
-def test_prologue_vt_lane_masks_equals_two_launches(dev, B, T, H):
+def test_prologue_vt_lane_masks_equals_two_launches(dev, B, T, H, causal):
     """gsa_prologue_vt_lane_masks (producer and lane masks in one launch, blocks
     interleaved) writes exactly what gsa_prologue_vt and gsa_dense_lane_masks write."""
-    _log(f"prologue_vt+lane masks B={B} T={T} H={H}")
+    _log(f"prologue_vt+lane masks B={B} T={T} H={H} causal={causal}")
     g = torch.Generator().manual_seed(T + H)
     k = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16).to(dev)
     v = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16).to(dev)
@@ -685,9 +700,12 @@ def test_prologue_vt_lane_masks_equals_two_launches(dev, B, T, H):
     idx, mask = orc.select_topk(s, min(40, T))
     bits = _abi.selection_mask(idx.to(torch.int32).to(dev), T, mask=mask.to(dev))
     ko, vt = _abi.prologue_vt(v, vg, k=k, cos=cos, sin=sin)
-    lm = _abi.dense_lane_masks(bits, T)
-    ko2, vt2, lm2 = _abi.prologue_vt(v, vg, k=k, cos=cos, sin=sin, bits=bits, Tkv=T)
+    nbytes = _abi.load().gsa_dense_attn_workspace_bytes(B, T, T)
+    lm = _abi.dense_lane_masks(bits, T, ws=torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=dev),
+                               causal=causal)
+    ko2, vt2, lm2 = _abi.prologue_vt(v, vg, k=k, cos=cos, sin=sin, bits=bits, Tkv=T, causal=causal,
+                                     ws=torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=dev))
     torch.cuda.synchronize()
     assert torch.equal(ko.cpu(), ko2.cpu()) and torch.equal(vt.cpu(), vt2.cpu())
-    # the masks cover every (group, causal tile) the attention reads; both calls write the same words
+    # both calls write the same words (and, causal, leave the same tiles unwritten)
     assert torch.equal(lm.cpu(), lm2.cpu())
