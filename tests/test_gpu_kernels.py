@@ -533,15 +533,15 @@ def test_dense_attention_noncausal_selection(dev):
     assert (torch.linalg.vector_norm(out.double() - ref) / torch.linalg.vector_norm(ref)).item() < 5e-3
 
 
-def _long_keys_case(T, Tkv, H, k, seed, causal, key_limit=None):
-    """q [1,T,H,d], k/v [1,Tkv,H,d] and k selected keys per row: random
+def _long_keys_case(T, Tkv, H, k, seed, causal, key_limit=None, B=1):
+    """q [B,T,H,d], k/v [B,Tkv,H,d] and k selected keys per row: random
     among the row's causal prefix (causal) or among all keys below key_limit."""
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn(1, T, H, 128, generator=g).to(torch.bfloat16)
-    kk = torch.randn(1, Tkv, H, 128, generator=g).to(torch.bfloat16)
-    v = torch.randn(1, Tkv, H, 128, generator=g).to(torch.bfloat16)
-    og = torch.randn(1, T, H, 128, generator=g).to(torch.bfloat16)
-    s = torch.rand(1, T, Tkv, generator=g)
+    q = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    kk = torch.randn(B, Tkv, H, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Tkv, H, 128, generator=g).to(torch.bfloat16)
+    og = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16)
+    s = torch.rand(B, T, Tkv, generator=g)
     if causal:
         s = s.masked_fill(torch.arange(Tkv)[None, None, :] > torch.arange(T)[None, :, None], float("-inf"))
     if key_limit is not None:
@@ -557,15 +557,16 @@ def _vt_of(v, dev):
     return vt
 
 
-@pytest.mark.parametrize("T,Tkv,H,k,causal", [(800, 33000, 2, 300, False), (800, 33000, 2, 300, True),
-                                              (385, 32768, 1, 64, False)])
-def test_dense_attention_long_keys_vs_oracle(dev, T, Tkv, H, k, causal):
+@pytest.mark.parametrize("B,T,Tkv,H,k,causal", [(1, 800, 33000, 2, 300, False), (1, 800, 33000, 2, 300, True),
+                                                (1, 385, 32768, 1, 64, False), (2, 400, 32768, 3, 96, True)])
+def test_dense_attention_long_keys_vs_oracle(dev, B, T, Tkv, H, k, causal):
     """From 32768 keys on gsa_dense_attn runs 12-wave (384-row) blocks: ragged
     query blocks (T = 2*384 + 32, 384 + 1), a ragged last key tile (33000 =
     515*64 + 40), causal and non-causal selections, RoPE(q) and the output gate,
-    against the float64 oracle with the bound of the short-key test."""
-    _log(f"dense_attn long keys T={T} Tkv={Tkv} H={H} k={k} causal={causal}")
-    q, kk, v, og, ia, cnt = _long_keys_case(T, Tkv, H, k, seed=T + Tkv, causal=causal)
+    against the float64 oracle with the bound of the short-key test; a batch of
+    two sequences checks the per-sequence offsets."""
+    _log(f"dense_attn long keys B={B} T={T} Tkv={Tkv} H={H} k={k} causal={causal}")
+    q, kk, v, og, ia, cnt = _long_keys_case(T, Tkv, H, k, seed=T + Tkv, causal=causal, B=B)
     cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
     bits = _abi.selection_mask(ia.to(dev), Tkv, count=cnt.to(dev))
     flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
@@ -655,7 +656,7 @@ def _lane_masks_expected(bits, T, Tkv):
 @pytest.mark.parametrize("B,T,Tkv,density", [(2, 300, 300, 0.5), (1, 777, 1000, 0.1), (1, 64, 64, 0.9),
                                              (3, 520, 130, 0.03),
                                              # 384-row blocks (12 groups) from 32768 keys on
-                                             (1, 400, 32800, 0.01)])
+                                             (1, 400, 32800, 0.01), (2, 390, 32800, 0.01)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_dense_lane_masks_layout(dev, B, T, Tkv, density, causal):
     """gsa_dense_lane_masks against the layout stated from the bitmask, on a random
