@@ -10,8 +10,8 @@
 // key j is selected and valid for query t.
 //
 // Per block: one head, 256 query rows (8 waves of 32 rows; 384 rows in 12
-// waves from 32K keys on), 64-key tiles in LDS.  With v_mfma_f32_32x32x16_bf16 both products are computed
-// transposed,
+// waves from 32K keys on), 64-key tiles in LDS.  With
+// v_mfma_f32_32x32x16_bf16 both products are computed transposed,
 //   S^T = K Q^T    (A = K tile from LDS, B = this wave's q, in registers)
 //   O^T = V^T P^T  (A = V^T tile from LDS, B = P in registers)
 // so in both outputs lane l holds column l%32 = one query row: a query's
@@ -247,10 +247,10 @@ __global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p,
 // Dense masked attention (bf16)
 //
 // Block: W waves = 32W query rows of one head (wave w: rows 32w .. 32w+31):
-// 8 waves (two per SIMD) or 12 (three per SIMD), by dense_block_waves.  K and V^T tiles reach LDS by direct
-// global->LDS loads (16 B per lane; one instruction fills 1 KiB,
-// lane-linear), K tiles and V^T tiles each through a pair of slots, in padded
-// layouts (unit = 16 B = 8 bf16):
+// 8 waves (two per SIMD) or 12 (three per SIMD), by dense_block_waves.  K
+// and V^T tiles reach LDS by direct global->LDS loads (16 B per lane; one
+// instruction fills 1 KiB, lane-linear), K tiles and V^T tiles each through a
+// pair of slots, in padded layouts (unit = 16 B = 8 bf16):
 //   K   tile: 64 keys x 17 units, unit 16 of a key is padding
 //   V^T tile: 128 rows x 9 units (64 keys), unit 8 of a row is padding
 // The odd row strides make every MFMA operand read conflict-free (16 lanes
