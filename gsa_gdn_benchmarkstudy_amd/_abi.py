@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgsa_hip.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -502,6 +502,7 @@ def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None, bits=Non
                                         ldv, _ptr(bits), bits.stride(0), bits.stride(1), Tkv, int(bool(causal)),
                                         _ptr(ws), nbytes, _stream(v))
     _check(st, "gsa_prologue_vt_lane_masks")
+    _tag_masks(ws, causal)
     return k_out, vt, ws
 
 
@@ -588,8 +589,15 @@ def selection_mask(idx, Tkv: int, count=None, mask=None, out=None):
     return out
 
 
+def _tag_masks(ws: torch.Tensor, causal: bool) -> None:
+    # Masks built for a causal attention leave the tiles past each query
+    # block's last row unwritten: record it on the tensor, so that dense_attn
+    # refuses them for a call that reads every tile.
+    ws._gsa_causal_masks = bool(causal)
+
+
 def dense_lane_masks(bits, Tkv: int, ws: Optional[torch.Tensor] = None, causal: bool = False) -> torch.Tensor:
-    """Lane masks of the dense attention from the selection bitmask [B,T,W] -> the
+    """Mask operands of the dense attention from the selection bitmask [B,T,W] -> the
     workspace tensor holding them (pass it to dense_attn with masks_ready=True).
     ``causal``: only the tiles a causal dense_attn reads, up to the last row of each
     query block (such masks serve causal calls only); otherwise every tile."""
@@ -604,6 +612,7 @@ def dense_lane_masks(bits, Tkv: int, ws: Optional[torch.Tensor] = None, causal: 
     st = lib.gsa_dense_lane_masks(_ptr(bits), bits.stride(0), bits.stride(1), B, T, Tkv, int(bool(causal)),
                                   _ptr(ws), nbytes, _stream(bits))
     _check(st, "gsa_dense_lane_masks")
+    _tag_masks(ws, causal)
     return ws
 
 
@@ -624,6 +633,9 @@ def dense_attn(q, k, vt, bits, scale: float, og=None, cos=None, sin=None, flags:
             "vt: [B,H,d,ldv] rows of ldv >= Tkv rounded up to 64")
     _expect(tuple(bits.shape) == (B, T, mask_words(Tkv)) and bits.stride(2) == 1, "bits: [B,T,W]")
     _expect(not masks_ready or ws is not None, "masks_ready needs the workspace that holds the masks")
+    _expect(not (masks_ready and not causal and getattr(ws, "_gsa_causal_masks", False)),
+            "masks_ready: these masks were built for a causal attention (tiles past each query block are "
+            "unwritten) and cannot serve a non-causal call")
     if og is not None:
         _expect(tuple(og.shape) == (B, T, H, d) and og.dtype == q.dtype, "og: [B,T,H,d] in q's dtype")
     if flags & ATTN_ROPE_Q:

@@ -129,101 +129,73 @@ __global__ __launch_bounds__(256) void selection_mask_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Selection bitmask -> per-lane masks of the dense kernel's score slots.
-// For 32-row group g (rows 32g + i), 64-key tile kt and score slot
-// s = 16c + r (c = 0,1; r = 0..15), lm[b][g][kt][s] bit (32h + i) is the
-// selection bit of row 32g+i and key 64kt + 32c + 16(r/8) + 8h + r%8 -- the
-// key that accumulator r of lane (h, i) holds in the S^T MFMA output of half
-// c (see the key order below).  One wave per (b, g, 4 consecutive tiles):
-// lane (h, i) reads row 32g+i's four 64-bit words and keeps keys 32h..32h+31
-// of each; a 32x32 bit transpose in each half of the wave turns the rows into
-// key columns (lane k: bit i = row 32g+i's bit of key k), and slot lane s
-// takes its two columns; lanes 0..31 write each tile's 256 contiguous bytes.
+// Selection bitmask -> the dense kernel's mask operands.
+// The dense kernel applies the selection inside its S^T accumulators: each
+// 32-key half starts with one v_mfma_scale_f32_32x32x64_f8f6f4 on e2m1 (fp4)
+// operands, an identity A (lane (h, m) of half c holds 1.0 at the k position
+// of the key that MFMA row m holds, when h == c) times a mask B scaled by
+// 2^kMaskExp, so the accumulator starts at +0 for a selected key and at
+// -6 * 2^kMaskExp for any other; the bf16 products then add onto that.
+// For 32-row group g (rows 32g + n), 64-key tile kt and lane l = 32h + n of
+// the wave that owns the group, mop[b][g][kt][l] (16 bytes) is that B operand:
+// nibble i (bits 4i .. 4i+3 of the 128-bit value) is 0x0 (+0.0) if row 32g+n
+// selects key 64kt + 32h + i, else 0xF (-6.0).  One 1 KiB record per
+// (group, tile), in the order the kernel's wave stages it into LDS.
+// One thread per (row, 4 consecutive tiles): it reads the row's 32 bytes of
+// selection words and writes lanes n and 32 + n of each tile's record.
 // ---------------------------------------------------------------------------
 constexpr int kLmTiles = 4;
-
-// 32x32 bit transpose inside each 32-lane half of the wave: on entry lane i
-// of a half holds row i (bit j = element (i, j)), on exit lane j holds
-// column j (bit i = element (i, j)).  Stage b (16, 8, 4, 2, 1) swaps the
-// off-diagonal b x b blocks of every 2b x 2b block between lanes i and i ^ b:
-// the lane with bit b clear keeps the low b bits of each 2b-bit group and
-// takes its partner's low ones, shifted up by b, into the high b; the other
-// lane keeps the high b bits and takes its partner's high ones shifted down.
-// Both shifts are one right rotation of the partner's word (by 32 - b or by
-// b: the bits that wrap around land in the part the lane keeps), so a stage
-// is a lane swizzle, a rotate and a bit select with per-lane constants.
-struct BitTranspose {
-  uint32_t keep[5], rot[5];   // per stage: bits the lane keeps, right rotation of the partner's word
-  __device__ explicit BitTranspose(int lane) {
-    constexpr uint32_t kLow[5] = {0x0000ffffu, 0x00ff00ffu, 0x0f0f0f0fu, 0x33333333u, 0x55555555u};
-#pragma unroll
-    for (int st = 0; st < 5; ++st) {
-      const int b = 16 >> st;
-      const bool up = (lane & b) != 0;
-      keep[st] = up ? ~kLow[st] : kLow[st];
-      rot[st] = up ? (uint32_t)b : (uint32_t)(32 - b);
-    }
-  }
-  // ds_swizzle bit mode (and 0x1f, or 0, xor B): lane ^ B within its 32-lane half
-  template <int St>
-  __device__ __forceinline__ uint32_t stage(uint32_t x) const {
-    constexpr int B = 16 >> St;
-    const uint32_t y = (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, (B << 10) | 0x1f);
-    const uint32_t sh = __builtin_amdgcn_alignbit(y, y, rot[St]);
-    return (x & keep[St]) | (sh & ~keep[St]);
-  }
-  __device__ __forceinline__ uint32_t operator()(uint32_t x) const {
-    return stage<4>(stage<3>(stage<2>(stage<1>(stage<0>(x)))));
-  }
-};
+constexpr int kMaskExp = 120;          // unselected keys start at -6 * 2^120 (about -8e36)
+constexpr float kNoKey = -1e36f;       // a tile row max below this: no selected key in the tile
 
 struct LaneMaskArgs {
   const uint32_t* bits; int64_t b_sb, b_st;
-  int T, G, NT, nwaves;
-  int block_rows;   // causal: query rows per attention block (tiles past a block's last row are skipped); else 0
-  uint64_t* lm;
+  int T, G, NT, nunits;   // unit = (batch, 32-row group, kLmTiles tiles): 32 threads
+  int block_rows;         // causal: query rows per attention block (tiles past a block's last row are skipped); else 0
+  u32x4* lm;
 };
 
-// Block `blk` of the lane-mask pass: its 4 waves take waves 4*blk .. 4*blk+3.
+// Bit i of an 8-bit value moved to bit 4i.
+__device__ __forceinline__ uint32_t spread_nibbles(uint32_t byte) {
+  uint32_t t = (byte | (byte << 12)) & 0x000F000Fu;
+  t = (t | (t << 6)) & 0x03030303u;
+  return (t | (t << 3)) & 0x11111111u;
+}
+// 32 selection bits -> 32 e2m1 nibbles: 0x0 where the bit is set, 0xF where not.
+__device__ __forceinline__ u32x4 mask_nibbles(uint32_t word) {
+  const uint32_t un = ~word;
+  u32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r[j] = spread_nibbles((un >> (8 * j)) & 0xffu) * 15u;
+  return r;
+}
+
+// Block `blk` of the mask-operand pass: its 256 threads take units 8*blk .. 8*blk+7.
 __device__ __forceinline__ void lane_mask_block(const LaneMaskArgs& a, int blk) {
-  const uint32_t* __restrict__ bits = a.bits;
-  uint64_t* __restrict__ lm = a.lm;
-  const int64_t b_sb = a.b_sb, b_st = a.b_st;
-  const int T = a.T, G = a.G, NT = a.NT;
-  const int wv = blk * 4 + (threadIdx.x >> 6);
-  if (wv >= a.nwaves) return;
-  const int nq = (NT + kLmTiles - 1) / kLmTiles;
-  const int kq = wv % nq, bg = wv / nq;
-  const int g = bg % G, b = bg / G;
-  const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
-  const int row = 32 * g + i;
+  const int gt = blk * 256 + (int)threadIdx.x;
+  const int unit = gt >> 5, n = gt & 31;
+  if (unit >= a.nunits) return;
+  const int nq = (a.NT + kLmTiles - 1) / kLmTiles;
+  const int kq = unit % nq, bg = unit / nq;
+  const int g = bg % a.G, b = bg / a.G;
+  const int row = 32 * g + n;
   const int kt0 = kq * kLmTiles;
   // Tiles the attention reads for this group: all of them, or (causal) those
   // up to the last row of the group's attention block, as its block does.
-  int nt = NT;
-  if (a.block_rows) nt = min(NT, ((32 * g) / a.block_rows + 1) * a.block_rows / kDK);
+  int nt = a.NT;
+  if (a.block_rows) nt = min(a.NT, ((32 * g) / a.block_rows + 1) * a.block_rows / kDK);
   if (kt0 >= nt) return;
+  const uint64_t* src =
+      reinterpret_cast<const uint64_t*>(a.bits + b * a.b_sb + (int64_t)min(row, a.T - 1) * a.b_st) + kt0;
   uint64_t words[kLmTiles];
-  const uint64_t* src = reinterpret_cast<const uint64_t*>(bits + b * b_sb + (int64_t)min(row, T - 1) * b_st) + kt0;
 #pragma unroll
-  for (int u = 0; u < kLmTiles; ++u) words[u] = (row < T && kt0 + u < nt) ? src[u] : 0ull;
-  // slot s = 16c + r (lane s < 32) holds key k0 = 32c + 16(r/8) + r%8 in its
-  // low 32 bits (lanes h = 0) and key k0 + 8 in its high 32 bits (h = 1)
-  const int s = lane & 31, k0 = 32 * (s >> 4) + 16 * ((s >> 3) & 1) + (s & 7);
-  const BitTranspose transpose(lane);
+  for (int u = 0; u < kLmTiles; ++u) words[u] = (row < a.T && kt0 + u < nt) ? src[u] : 0ull;
 #pragma unroll
   for (int u = 0; u < kLmTiles; ++u) {
     if (kt0 + u >= nt) break;
-    uint64_t out = 0;
-    // A tile no row of the group selects from (every tile past the group's
-    // diagonal, for a causal selection) has all-zero masks: no transpose.
-    if (ballot64(words[u] != 0ull)) {
-      const uint32_t col = transpose((uint32_t)(words[u] >> (32 * h)));   // key `lane`'s column
-      const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * k0, (int)col);
-      const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (k0 + 8), (int)col);
-      out = ((uint64_t)hi << 32) | lo;
-    }
-    if (lane < 32) lm[((int64_t)bg * NT + kt0 + u) * 32 + lane] = out;
+    u32x4* dst = a.lm + ((int64_t)bg * a.NT + kt0 + u) * 64;
+    dst[n] = mask_nibbles((uint32_t)words[u]);
+    dst[32 + n] = mask_nibbles((uint32_t)(words[u] >> 32));
   }
 }
 
@@ -248,11 +220,13 @@ __global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p,
 //
 // Block: W waves = 32W query rows of one head (wave w: rows 32w .. 32w+31):
 // 8 waves (two per SIMD) or 12 (three per SIMD), by dense_block_waves.  K
-// and V^T tiles reach LDS by direct global->LDS loads (16 B per lane; one
-// instruction fills 1 KiB, lane-linear), K tiles and V^T tiles each through a
-// pair of slots, in padded layouts (unit = 16 B = 8 bf16):
+// and V^T tiles and each wave's mask operands reach LDS by direct
+// global->LDS loads (16 B per lane; one instruction fills 1 KiB,
+// lane-linear), each through a pair of slots, K and V^T in padded layouts
+// (unit = 16 B = 8 bf16):
 //   K   tile: 64 keys x 17 units, unit 16 of a key is padding
 //   V^T tile: 128 rows x 9 units (64 keys), unit 8 of a row is padding
+//   mask:     W waves x 64 units (each lane's 16-byte B operand)
 // The odd row strides make every MFMA operand read conflict-free (16 lanes
 // reading one unit of 16 different rows hit 16 different bank groups), and
 // each operand read is one base register plus an immediate offset.  Padding
@@ -261,19 +235,25 @@ __global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p,
 // pi(rho), pi swapping bits 2 and 3 of rho, so accumulator r of lane (h, i)
 // holds key 16(r/8) + 8h + r%8.  A lane's 8 P values of each 16-key k-step
 // are then contiguous keys, and its V^T operand is one 16-byte read.
+// Masking: each half's S^T accumulators start from the fp4 mask product
+// (+0 selected, about -8e36 not selected; lane_mask_block), so the softmax
+// takes its row max and exponentials straight from the accumulators: a
+// key that is not selected gets p = 2^(-huge) = 0, and the scores of the
+// selected keys are the bf16 products alone, bit for bit.  No mask word
+// passes through scalar registers and the loop issues no scalar load.
 //
 // Tiles are pipelined (8 waves): S^T of tile t+1 is computed, one 32-key
-// half at a time, while tile t's scores are masked half by half (each half
-// with its own 16 lane-mask words), then the tile's one online-softmax
-// decision with the lazy reference (below), then O^T += V^T(t) P^T(t) half by
-// half, so MFMA and VALU work of one wave overlap.  12-wave blocks compute
-// S^T(t) itself in that place (one S accumulator pair per wave).
+// half at a time, while tile t's row maxima are taken, then the tile's one
+// online-softmax decision with the lazy reference (below), then O^T +=
+// V^T(t) P^T(t) half by half, so MFMA and VALU work of one wave overlap.
+// 12-wave blocks compute S^T(t) itself in that place (one S accumulator pair
+// per wave).
 // ---------------------------------------------------------------------------
 struct DenseArgs {
   const uint16_t* q; int64_t q_sb, q_st;
   const uint16_t* k; int64_t k_sb, k_st;
   const uint16_t* vt; int64_t vt_sb, vt_sh; int ldv;
-  int G, NT;                              // lane masks [B][G][NT][32] (kernel argument)
+  int G, NT;                              // mask operands [B][G][NT][64] u32x4 (kernel argument)
   const uint16_t* og; int64_t o_sb, o_st;
   const uint16_t* cos; const uint16_t* sin; int64_t cs_st;
   uint16_t* out; int64_t out_sb, out_st;
@@ -289,9 +269,12 @@ constexpr int kKU = kDK * kKRow;       // 1088 units: K tile
 constexpr int kVU = 128 * kVRow;       // 1152 units: V^T tile
 constexpr int kDmaK = kKU / 64;        // 17 load instructions fill a K tile
 constexpr int kDmaV = kVU / 64;        // 18 fill a V^T tile
-constexpr size_t kDenseLds = (size_t)2 * (kKU + kVU) * 16;   // two K slots, then two V^T slots
+constexpr int kMBase = 2 * (kKU + kVU);   // units: two K slots, two V^T slots, then the two mask slots
+// LDS of a W-wave block: the K and V^T slot pairs, then two mask slots of W KiB.
+__host__ __device__ constexpr size_t dense_lds_bytes(int W) { return (size_t)(kMBase + 2 * 64 * W) * 16; }
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef int intx8 __attribute__((ext_vector_type(8)));
 
 // Value of lane l^32 combined with the own value: permlane32_swap of (v, v)
 // leaves {v[l], v[l^32]} in the two results on every lane.  max_halves takes
@@ -336,38 +319,37 @@ __device__ __forceinline__ int swap_bits23(int i) { return (i & ~12) | ((i & 4) 
 template <int N> struct Int { static constexpr int value = N; };
 
 // Pipeline of one block (W waves = 32W query rows of one head), tile t = 64
-// keys.  K tiles and V^T tiles stream through separate pairs of LDS slots
-// (tile t in slot t&1).  With PP (ping-pong S), iteration t, after one
-// barrier:
-//   loads  K(t+2) into K slot t&1 (S(t) was computed last iteration) and
-//          V^T(t+1) into V slot (t+1)&1 (PV(t-1) is done);
-//   MFMA   S^T(t+1) from K slot (t+1)&1, interleaved with the softmax of
+// keys.  K tiles, V^T tiles and mask operands stream through separate pairs
+// of LDS slots (tile t in slot t&1).  With PP (ping-pong S), iteration t,
+// after one barrier:
+//   loads  K(t+2) and its mask operands into K / mask slot t&1 (S(t) was
+//          computed last iteration) and V^T(t+1) into V slot (t+1)&1 (PV(t-1)
+//          is done);
+//   MFMA   S^T(t+1) from K slot (t+1)&1, interleaved with the row maxima of
 //          S(t) (VALU), then O^T += V^T(t) P^T(t) from V slot t&1.
 // So the S product of the next tile overlaps the softmax of this one, within
 // the wave, at the cost of a second S accumulator pair (64 VGPRs).  Without
-// PP, iteration t loads K(t+1) and V^T(t+1) into slots (t+1)&1 and computes
-// S^T(t), its softmax and PV(t) from slots t&1: one S pair, so 12-wave blocks
-// (three waves per SIMD) fit the register file, and the overlap of MFMA and
-// VALU work comes from the other waves of the SIMD instead.  8 waves with PP
-// is the faster form up to 16K keys, 12 without PP beyond (fewer tile loads
-// per query row: at 65536 keys 17.1 -> 15.9 ms, K and V^T no longer fit the
-// last-level cache).  Every load is issued one iteration before the barrier
-// that publishes it; the loop is unrolled by two so that slot offsets are
-// constants.
-// lm is a separate restrict argument: nothing in this kernel writes it, and
-// alias analysis can see that, so its uniform reads stay scalar loads.
+// PP, iteration t loads K(t+1), V^T(t+1) and the mask operands of t+1 into
+// slots (t+1)&1 and computes S^T(t), its softmax and PV(t) from slots t&1:
+// one S pair, so 12-wave blocks (three waves per SIMD) fit the register
+// file, and the overlap of MFMA and VALU work comes from the other waves of
+// the SIMD instead.  8 waves with PP is the faster form up to 16K keys, 12
+// without PP beyond (fewer tile loads per query row: at 65536 keys 17.1 ->
+// 15.9 ms, K and V^T no longer fit the last-level cache).  Every load is
+// issued one iteration before the barrier that publishes it; the loop is
+// unrolled by two so that slot offsets are constants.
 template <int W, bool PP>
-__global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, const uint64_t* __restrict__ lm) {
-  extern __shared__ __align__(16) u32x4 dsm[];   // K slots 0, 1 (kKU units each), then V^T slots 0, 1 (kVU)
+__global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, const u32x4* __restrict__ lm) {
+  extern __shared__ __align__(16) u32x4 dsm[];   // K slots 0, 1 (kKU units each), V^T slots 0, 1 (kVU), mask slots 0, 1 (64W)
   constexpr int kDW = W;                          // waves per block
   constexpr int kDQ = 32 * W;                     // query rows per block
   constexpr int kDmaKW = (kDmaK + kDW - 1) / kDW;   // K instructions per wave (wave w: i = kDW*n + w < 17)
   constexpr int kDmaVW = (kDmaV + kDW - 1) / kDW;   // V^T instructions per wave
+  constexpr int kMSlot = 64 * kDW;                // units of one mask slot
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(w);
   const int i32 = lane & 31, h = lane >> 5;
-  // heaviest query blocks first
   // Block order: batch by batch (the blocks in flight then share one
   // sequence's K and V^T, which stays in the last-level cache), within a
   // sequence the heaviest query blocks first, heads fastest.
@@ -392,7 +374,8 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
   // 64i .. 64i+63 (key u/17, unit u%17), V^T instruction i units 64i .. (row
   // u/9, unit u%9).  koff/voff = this lane's source byte offset from the
   // tile's K or V^T base (32-bit: the host bounds k_st and ldv); koff_last
-  // for the last tile, whose keys past Tkv-1 re-read key Tkv-1.
+  // for the last tile, whose keys past Tkv-1 re-read key Tkv-1.  Each wave
+  // also loads its own group's 1 KiB of mask operands per tile.
   const int nkw = (kDmaK - 1 - wu) / kDW + 1;    // this wave's K instructions (uniform)
   const int nvw = (kDmaV - 1 - wu) / kDW + 1;    // and V^T instructions
   uint32_t koff[kDmaKW], koff_last[kDmaKW], voff[kDmaVW];
@@ -417,6 +400,10 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
   }
   const uint32_t kdst = lds0 + (uint32_t)wu * 1024u;                      // + slot * kKU * 16 + n * kDW KiB
   const uint32_t vdst = lds0 + (uint32_t)(2 * kKU * 16) + (uint32_t)wu * 1024u;
+  const uint32_t mdst = lds0 + (uint32_t)(kMBase * 16) + (uint32_t)wu * 1024u;   // + slot * kDW KiB
+  // this wave's mask operands: group kDW*qb + w, 1 KiB per tile
+  const char* mbase = reinterpret_cast<const char*>(lm + ((int64_t)b * p.G + kDW * qb + wu) * p.NT * 64);
+  const uint32_t moff = (uint32_t)lane * 16u;
   auto issue_k = [&](const char* src, int slot, bool last) {   // one K tile into K slot `slot`
 #pragma unroll
     for (int n = 0; n < kDmaKW; ++n)
@@ -429,9 +416,16 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
       if (n + 1 < kDmaVW || n < nvw)
         load_lds16(src, voff[n], vdst + (uint32_t)(slot * kVU * 16 + n * kDW * 1024));
   };
-  // prologue loads: K(0), K(1) (ping-pong only), V(0)
+  auto issue_m = [&](int kt, int slot) {                       // tile kt's mask operands into mask slot `slot`
+    load_lds16(mbase + (int64_t)kt * 1024, moff, mdst + (uint32_t)(slot * kDW * 1024));
+  };
+  // prologue loads: K(0), K(1) (ping-pong only), V(0) and the mask operands of the same tiles
   issue_k(kbase, 0, nkt == 1);
-  if (PP && nkt > 1) issue_k(kbase + kstep, 1, nkt == 2);
+  issue_m(0, 0);
+  if (PP && nkt > 1) {
+    issue_k(kbase + kstep, 1, nkt == 2);
+    issue_m(1, 1);
+  }
   issue_v(vtb, 0);
 
   // ---- q: B operand of S^T; lane supplies d = 16s + 8h .. +7 of its row ----
@@ -470,6 +464,19 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
 #pragma unroll
   for (int s = 0; s < 8; ++s) qop[s] = __builtin_bit_cast(bf16x8, qraw[s]);
 
+  // Identity A operands of the mask products (e2m1 1.0 = 0x2): half c, lane
+  // (h, m): the k position of key pi(m) of the half -- position pi(m) of the
+  // lane's 32 -- when h == c, nothing otherwise.  Only the first four
+  // registers of an fp4 operand are read.
+  intx8 ident[2];
+  {
+    const int pos = swap_bits23(i32);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ident[c][j] = (h == c && j == (pos >> 3)) ? (2 << (4 * (pos & 7))) : 0;
+  }
+
   floatx16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -480,14 +487,18 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
   float m = -__builtin_inff(), mlz = -__builtin_inff(), nm = 0.f, l = 0.f;
   const bf16x2 ones2 = __builtin_bit_cast(bf16x2, 0x3f803f80u);   // (1, 1)
 
-  // this wave's lane masks: group kDW*qb + w (wave index uniform for scalar loads)
-  const uint64_t* lmw = lm + ((int64_t)b * p.G + kDW * qb + wu) * p.NT * 32;
-  // operand read offsets (units within a slot): K row of MFMA row i32, V^T row i32
+  // operand read offsets (units within a slot): K row of MFMA row i32, V^T row i32, own mask operand
   const int kread = swap_bits23(i32) * kKRow + h;
   const int vread = 2 * kKU + i32 * kVRow + h;
+  const int mread = kMBase + wu * 64 + lane;
 
-  // S^T of one 32-key half of the tile in K slot ks
-  auto s_half = [&](int ks, int c) {
+  // the mask operands of the tile in mask slot ms (B operand, fp4: first four registers)
+  auto mask_op = [&](int ms) {
+    const u32x4 v = dsm[mread + ms * kMSlot];
+    return intx8{(int)v[0], (int)v[1], (int)v[2], (int)v[3], 0, 0, 0, 0};
+  };
+  // S^T of one 32-key half of the tile in K slot ks, starting from its mask product
+  auto s_half = [&](int ks, int c, const intx8& mop) {
     const u32x4* sK = dsm + ks * kKU + kread;
     bf16x8 f[8];
 #pragma unroll
@@ -495,48 +506,34 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ident[c], mop, acc, 4, 4, 0, 127, 0, 127 + kMaskExp);
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[s], qop[s], acc, 0, 0, 0);
     return acc;
   };
   // Masked online softmax, one step per 64-key tile: p = 2^(s*scale*log2e -
   // m) against a per-row reference m that only moves when the tile's row max
-  // exceeds it by more than kLazy (p <= 2^kLazy; out = O / l does not depend
-  // on m).  mask_half keeps the selected scores of one 32-key half (the others
-  // -inf) and returns their max; both halves are masked before the tile's one
-  // reference decision, so their lane-mask loads and the S^T MFMAs of the next
-  // tile share one stretch of code.  A move is rare: its bookkeeping --
-  // alpha = 2^(m_old - m_new), O and l times alpha, the new m, m + kLazy and
-  // -m -- runs in a branch the wave takes only when one of its rows moves.
+  // over its selected keys exceeds it by more than kLazy (p <= 2^kLazy; out =
+  // O / l does not depend on m).  max_half takes a half's maximum straight
+  // from its accumulators (a key that is not selected sits near -8e36 there);
+  // both halves are taken before the tile's one reference decision, so the S^T
+  // MFMAs of the next tile share that stretch of code.  A maximum below kNoKey
+  // means no selected key.  A move is rare: its bookkeeping -- alpha =
+  // 2^(m_old - m_new), O and l times alpha, the new m, m + kLazy and -m --
+  // runs in a branch the wave takes only when one of its rows moves.
   // exp_half turns a half's scores into P (two B operands of O^T) and adds
   // the bf16 values that the PV product uses to l, one dot2 per pair.
-  // (mask_half_r takes the half's 16 mask words from registers, mask_half
-  // loads them from the lane-mask array where they are used)
-  auto mask_half_r = [&](const floatx16& acc, const uint64_t (&mw)[16], float (&sv)[16]) -> float {
+  auto max_half = [&](const floatx16& acc) -> float {
     float mx = -__builtin_inff();
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const bool sel = __builtin_amdgcn_inverse_ballot_w64(mw[r]);
-      sv[r] = sel ? acc[r] : -__builtin_inff();
-      mx = fmaxf(mx, sv[r]);
-    }
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[r]);
     return mx;                                      // never NaN: the max is seeded with -inf
   };
-  auto mask_half = [&](const floatx16& acc, const uint64_t* lmt, int c, float (&sv)[16]) -> float {
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const bool sel = __builtin_amdgcn_inverse_ballot_w64(lmt[16 * c + r]);
-      sv[r] = sel ? acc[r] : -__builtin_inff();
-      mx = fmaxf(mx, sv[r]);
-    }
-    return mx;                                      // never NaN: the max is seeded with -inf
-  };
-  auto exp_half = [&](const float (&sv)[16], uint32_t (&pk)[2][4]) {
+  auto exp_half = [&](const floatx16& acc, uint32_t (&pk)[2][4]) {
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], p.scale_l2, nm));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r + 1], p.scale_l2, nm));
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], p.scale_l2, nm));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r + 1], p.scale_l2, nm));
       const uint32_t w = pack_bf16(p0, p1);
       pk[r >> 3][(r & 7) >> 1] = w;
       l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones2, l, false);
@@ -571,21 +568,11 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   const char* vsrc = vtb + kDK * 2;                  // V^T tile kt+1
-  const uint64_t* lmt = lmw;                         // lane masks of tile kt
-  // The first half's 16 lane-mask words of a tile are loaded one iteration
-  // ahead, after the previous tile's masks are used, so their scalar loads
-  // are in flight during the PV products and done at the next barrier (at
-  // T=65536 the masks come from HBM; with 8-wave blocks 18.3 -> 17.0 ms).
-  // The second half's are loaded where they are used: holding both halves
-  // ahead would need 32 more SGPRs and spills 130 of them.
-  uint64_t mw0[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) mw0[r] = lmw[r];
-  // Tile kt once both halves are masked (scores sv0, sv1, maxima mx0, mx1):
-  // the softmax decision, P, O^T += V^T(kt) P^T(kt) from V slot vs, and the
-  // next tile's first-half mask words.
-  auto softmax_pv = [&](int kt, int vs, float mx0, float mx1, const float (&sv0)[16], const float (&sv1)[16]) {
-    const float mx = max_halves(mx1 > mx0 ? mx1 : mx0) * p.scale_l2;
+  // Tile kt once both halves' maxima are taken: the softmax decision, P and
+  // O^T += V^T(kt) P^T(kt) from V slot vs.
+  auto softmax_pv = [&](int vs, float mx0, float mx1, const floatx16& s0, const floatx16& s1) {
+    float mx = max_halves(mx1 > mx0 ? mx1 : mx0);
+    mx = mx > kNoKey ? mx * p.scale_l2 : -__builtin_inff();
     // mx > m + kLazy; while m = -inf: any selected key
     if (ballot64(mx > mlz)) {
       const bool bump = mx > mlz;
@@ -597,42 +584,45 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
       nm = m == -__builtin_inff() ? 0.f : -m;
     }
     uint32_t pk0[2][4], pk1[2][4];
-    exp_half(sv0, pk0);
+    exp_half(s0, pk0);
     pv_half(vs, 0, pk0);
-    exp_half(sv1, pk1);
+    exp_half(s1, pk1);
     pv_half(vs, 1, pk1);
-    if (kt + 1 < nkt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mw0[r] = lmt[32 + r];
-    }
-    lmt += 32;
   };
 
   if constexpr (PP) {
     // S^T of tile kt in sc[kt & 1]: with the loop unrolled by two, each
     // iteration writes the other pair, so no accumulator is copied
     floatx16 sc[2][2];
-    sc[0][0] = s_half(0, 0);
-    sc[0][1] = s_half(0, 1);                        // S^T of tile 0
+    {
+      const intx8 mop = mask_op(0);
+      sc[0][0] = s_half(0, 0, mop);
+      sc[0][1] = s_half(0, 1, mop);                 // S^T of tile 0
+    }
     const char* ksrc = kbase + 2 * kstep;            // K tile kt+2
     // one iteration; P = kt & 1
     auto step = [&](int kt, auto par) {
       constexpr int P = decltype(par)::value;
-      // this wave's loads of K(kt+1) and V^T(kt) (issued last iteration) are
-      // done and its LDS reads have returned; the barrier publishes every
-      // wave's loads and frees K slot P and V slot 1-P
+      // this wave's loads of K(kt+1), its mask operands and V^T(kt) (issued
+      // last iteration) are done and its LDS reads have returned; the
+      // barrier publishes every wave's loads and frees K and mask slot P and
+      // V slot 1-P
       asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (kt + 2 < nkt) issue_k(ksrc, P, kt + 3 == nkt);
+      if (kt + 2 < nkt) {
+        issue_k(ksrc, P, kt + 3 == nkt);
+        issue_m(kt + 2, P);
+      }
       if (kt + 1 < nkt) issue_v(vsrc, 1 - P);
       ksrc += kstep;
       vsrc += kDK * 2;
 
-      float sv0[16], sv1[16];
-      sc[1 - P][0] = s_half(1 - P, 0);             // S^T(kt+1) || softmax(kt); stale on the last tile, unused
-      const float mx0 = mask_half_r(sc[P][0], mw0, sv0);
-      sc[1 - P][1] = s_half(1 - P, 1);
-      const float mx1 = mask_half(sc[P][1], lmt, 1, sv1);
-      softmax_pv(kt, P, mx0, mx1, sv0, sv1);
+      // S^T(kt+1) || softmax(kt); stale on the last tile, unused
+      const intx8 mop = mask_op(1 - P);
+      sc[1 - P][0] = s_half(1 - P, 0, mop);
+      const float mx0 = max_half(sc[P][0]);
+      sc[1 - P][1] = s_half(1 - P, 1, mop);
+      const float mx1 = max_half(sc[P][1]);
+      softmax_pv(P, mx0, mx1, sc[P][0], sc[P][1]);
     };
     int t = 0;
     for (; t + 1 < nkt; t += 2) {
@@ -645,23 +635,25 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
     // one iteration; P = kt & 1
     auto step = [&](int kt, auto par) {
       constexpr int P = decltype(par)::value;
-      // this wave's loads of K(kt) and V^T(kt) (issued last iteration) are
-      // done and its LDS reads have returned; the barrier publishes every
-      // wave's loads and frees slots 1-P (tile kt-1) for tile kt+1
+      // this wave's loads of K(kt), V^T(kt) and its mask operands (issued
+      // last iteration) are done and its LDS reads have returned; the barrier
+      // publishes every wave's loads and frees slots 1-P (tile kt-1) for tile
+      // kt+1
       asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (kt + 1 < nkt) {
         issue_k(ksrc, 1 - P, kt + 2 == nkt);
         issue_v(vsrc, 1 - P);
+        issue_m(kt + 1, 1 - P);
       }
       ksrc += kstep;
       vsrc += kDK * 2;
 
-      float sv0[16], sv1[16];
-      const floatx16 s0 = s_half(P, 0);
-      const float mx0 = mask_half_r(s0, mw0, sv0);
-      const floatx16 s1 = s_half(P, 1);
-      const float mx1 = mask_half(s1, lmt, 1, sv1);
-      softmax_pv(kt, P, mx0, mx1, sv0, sv1);
+      const intx8 mop = mask_op(P);
+      const floatx16 s0 = s_half(P, 0, mop);
+      const float mx0 = max_half(s0);
+      const floatx16 s1 = s_half(P, 1, mop);
+      const float mx1 = max_half(s1);
+      softmax_pv(P, mx0, mx1, s0, s1);
     };
     int t = 0;
     for (; t + 1 < nkt; t += 2) {
@@ -776,11 +768,11 @@ int64_t dense_groups(int T, int Tkv) {
 }
 }  // namespace
 
-// Lane masks: 32 per (batch, 32-row group, 64-key tile); the groups are
-// counted over whole query blocks of the dense kernel.
+// Mask operands: 1 KiB (64 lanes x 16 bytes) per (batch, 32-row group, 64-key
+// tile); the groups are counted over whole query blocks of the dense kernel.
 extern "C" size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv) {
   if (B < 1 || T < 1 || Tkv < 1) return 0;
-  return (size_t)B * (size_t)dense_groups(T, Tkv) * ((Tkv + 63) / 64) * 32 * sizeof(uint64_t);
+  return (size_t)B * (size_t)dense_groups(T, Tkv) * ((Tkv + 63) / 64) * 1024;
 }
 
 namespace {
@@ -793,7 +785,10 @@ int lane_mask_checks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, in
   if (b_st < 2 * NT || (B > 1 && b_sb < (int64_t)T * b_st)) return GSA_ERR_SHAPE;
   if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
   if ((int64_t)B * dense_groups(T, Tkv) * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
-  if (!aligned(bits, 8) || (b_sb % 2) || (b_st % 2) || !aligned(ws, 8)) return GSA_ERR_ALIGN;
+  // one thread per (row, kLmTiles tiles): the thread index stays 32-bit
+  if ((int64_t)B * dense_groups(T, Tkv) * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles) * 32 > 0x7fffffffLL)
+    return GSA_ERR_SHAPE;
+  if (!aligned(bits, 8) || (b_sb % 2) || (b_st % 2) || !aligned(ws, 16)) return GSA_ERR_ALIGN;
   return GSA_OK;
 }
 
@@ -801,15 +796,15 @@ gsa::LaneMaskArgs lane_mask_args(const uint32_t* bits, int64_t b_sb, int64_t b_s
                                   int causal, void* ws) {
   const int NT = (Tkv + 63) / 64;
   const int G = (int)dense_groups(T, Tkv);
-  const int nwaves = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
+  const int nunits = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
   const int block_rows = causal ? 32 * gsa::dense_block_waves(Tkv) : 0;
-  return gsa::LaneMaskArgs{bits, b_sb, b_st, T, G, NT, nwaves, block_rows, static_cast<uint64_t*>(ws)};
+  return gsa::LaneMaskArgs{bits, b_sb, b_st, T, G, NT, nunits, block_rows, static_cast<gsa::u32x4*>(ws)};
 }
 
 int launch_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st, int B, int T, int Tkv, int causal,
                       void* ws, hipStream_t s) {
   const gsa::LaneMaskArgs l = lane_mask_args(bits, b_sb, b_st, B, T, Tkv, causal, ws);
-  hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((l.nwaves + 3) / 4), dim3(256), 0, s, l);
+  hipLaunchKernelGGL(gsa::lane_mask_kernel, dim3((l.nunits + 7) / 8), dim3(256), 0, s, l);
   return launch_status();
 }
 }  // namespace
@@ -838,7 +833,7 @@ extern "C" int gsa_prologue_vt_lane_masks(const void* k, int64_t k_sb, int64_t k
                    static_cast<const uint16_t*>(sin), cs_st, static_cast<uint16_t*>(k_out),
                    static_cast<uint16_t*>(vt), T, H, ldv, ldv / 64};
   const gsa::LaneMaskArgs l = lane_mask_args(bits, b_sb, b_st, B, T, Tkv, causal, ws);
-  const int n_pro = B * H * (ldv / 64), n_lm = (l.nwaves + 3) / 4;
+  const int n_pro = B * H * (ldv / 64), n_lm = (l.nunits + 7) / 8;
   if ((int64_t)n_pro + n_lm > 0x7fffffffLL) return GSA_ERR_SHAPE;
   hipLaunchKernelGGL(gsa::prologue_vt_lane_mask_kernel, dim3(n_pro + n_lm), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a, l, n_pro, n_lm);
@@ -873,7 +868,7 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   const int64_t G = dense_groups(T, Tkv);      // 32-row groups, padded to whole blocks
   if ((int64_t)B * H * nqb > 0x7fffffffLL || B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
   if (!vec_ok(q, q_sb, q_st, dtype) || !vec_ok(k, k_sb, k_st, dtype) || !vec_ok(vt, vt_sb, vt_sh, dtype) ||
-      !vec_ok(out, out_sb, out_st, dtype) || !aligned(ws, 8))
+      !vec_ok(out, out_sb, out_st, dtype) || !aligned(ws, 16))
     return GSA_ERR_ALIGN;
   if ((flags & GSA_ATTN_OUT_GATE) && !vec_ok(og, o_sb, o_st, dtype)) return GSA_ERR_ALIGN;
   if ((flags & GSA_ATTN_ROPE_Q) && (!vec_ok(cos, 0, cs_st, dtype) || !vec_ok(sin, 0, cs_st, dtype)))
@@ -883,7 +878,7 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
     if (st) return st;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  uint64_t* lm = static_cast<uint64_t*>(ws);
+  const gsa::u32x4* lm = static_cast<const gsa::u32x4*>(ws);
   if (!ready) {
     const int st = launch_lane_masks(bits, b_sb, b_st, B, T, Tkv, causal, ws, s);
     if (st) return st;
@@ -900,15 +895,15 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   const void* fn = wide ? reinterpret_cast<const void*>(gsa::dense_attn_kernel<12, false>)
                         : reinterpret_cast<const void*>(gsa::dense_attn_kernel<8, true>);
   if (!g_dense_lds_set[dev][wide]) {   // more than the default 64 KiB of LDS per block
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsa::kDenseLds);
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsa::dense_lds_bytes(W));
     if (e != hipSuccess) return -static_cast<int>(e);
     g_dense_lds_set[dev][wide] = true;
   }
   if (wide)
-    hipLaunchKernelGGL((gsa::dense_attn_kernel<12, false>), dim3(B * H * nqb), dim3(64 * 12), gsa::kDenseLds, s,
-                       a, static_cast<const uint64_t*>(lm));
+    hipLaunchKernelGGL((gsa::dense_attn_kernel<12, false>), dim3(B * H * nqb), dim3(64 * 12), gsa::dense_lds_bytes(12),
+                       s, a, lm);
   else
-    hipLaunchKernelGGL((gsa::dense_attn_kernel<8, true>), dim3(B * H * nqb), dim3(64 * 8), gsa::kDenseLds, s, a,
-                       static_cast<const uint64_t*>(lm));
+    hipLaunchKernelGGL((gsa::dense_attn_kernel<8, true>), dim3(B * H * nqb), dim3(64 * 8), gsa::dense_lds_bytes(8),
+                       s, a, lm);
   return launch_status();
 }

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define GSA_ABI_VERSION 2
+#define GSA_ABI_VERSION 3
 
 #define GSA_DTYPE_F32  0
 #define GSA_DTYPE_BF16 1

@@ -204,7 +204,7 @@ def test_dense_path_validation(lib):
     g = lib.gsa_dense_attn
     ok = dict(q=P, qsb=0, qst=2048, k=P, ksb=0, kst=2048, vt=P, vtsb=0, vtsh=8192, ldv=64, bits=P, bsb=0, bst=2,
               og=P, osb=0, ost=2048, cos=P, sin=P, cst=128, out=P, outsb=0, outst=2048,
-              B=1, T=4, Tkv=4, H=16, d=128, scale=0.088, dtype=1, flags=3, causal=1, ws=P, wsb=8 * 256)
+              B=1, T=4, Tkv=4, H=16, d=128, scale=0.088, dtype=1, flags=3, causal=1, ws=P, wsb=8 * 1024)
 
     def call(**kw):
         a = dict(ok)
@@ -214,28 +214,29 @@ def test_dense_path_validation(lib):
                  a["out"], a["outsb"], a["outst"], a["B"], a["T"], a["Tkv"], a["H"], a["d"], a["scale"],
                  a["dtype"], a["flags"], a["causal"], a["ws"], a["wsb"], None)
 
-    # 256 B of lane masks per (batch, 32-row group, 64-key tile); groups cover whole 256-row blocks
-    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 4) == 8 * 256
-    assert lib.gsa_dense_attn_workspace_bytes(2, 100, 130) == 2 * 8 * 3 * 256
-    assert lib.gsa_dense_attn_workspace_bytes(1, 257, 64) == 16 * 256
+    # 1 KiB of mask operands per (batch, 32-row group, 64-key tile); groups cover whole 256-row blocks
+    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 4) == 8 * 1024
+    assert lib.gsa_dense_attn_workspace_bytes(2, 100, 130) == 2 * 8 * 3 * 1024
+    assert lib.gsa_dense_attn_workspace_bytes(1, 257, 64) == 16 * 1024
     # from 32768 keys on the blocks hold 384 rows (12 groups)
     assert _abi.dense_block_rows(32767) == 256 and _abi.dense_block_rows(32768) == 384
-    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 32767) == 8 * 512 * 256
-    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 32768) == 12 * 512 * 256
-    assert lib.gsa_dense_attn_workspace_bytes(2, 385, 40000) == 2 * 24 * 625 * 256
+    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 32767) == 8 * 512 * 1024
+    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 32768) == 12 * 512 * 1024
+    assert lib.gsa_dense_attn_workspace_bytes(2, 385, 40000) == 2 * 24 * 625 * 1024
     assert call(bits=None) == 1
     assert call(ws=None) == 1
-    assert call(wsb=8 * 256 - 1) == 2             # workspace too small
+    assert call(wsb=8 * 1024 - 1) == 2            # workspace too small
     assert call(dtype=0) == 3                     # bf16 only
     assert call(ldv=32) == 2                      # rows shorter than ceil(Tkv/64)*64
     assert call(flags=8) == 6                     # unknown flag
     assert call(bst=3) == 4
     lmk = lib.gsa_dense_lane_masks
-    assert lmk(None, 0, 2, 1, 4, 4, 1, P, 8 * 256, None) == 1
-    assert lmk(P, 0, 2, 1, 4, 4, 1, None, 8 * 256, None) == 1
-    assert lmk(P, 0, 2, 1, 4, 4, 1, P, 8 * 256 - 1, None) == 2   # workspace too small
-    assert lmk(P, 0, 1, 1, 4, 4, 1, P, 8 * 256, None) == 2       # row of W words shorter than 2*ceil(Tkv/64)
-    assert lmk(P, 0, 3, 1, 4, 4, 1, P, 8 * 256, None) == 4       # 8-byte aligned rows
+    assert lmk(None, 0, 2, 1, 4, 4, 1, P, 8 * 1024, None) == 1
+    assert lmk(P, 0, 2, 1, 4, 4, 1, None, 8 * 1024, None) == 1
+    assert lmk(P, 0, 2, 1, 4, 4, 1, P, 8 * 1024 - 1, None) == 2   # workspace too small
+    assert lmk(P, 0, 1, 1, 4, 4, 1, P, 8 * 1024, None) == 2       # row of W words shorter than 2*ceil(Tkv/64)
+    assert lmk(P, 0, 3, 1, 4, 4, 1, P, 8 * 1024, None) == 4       # 8-byte aligned rows
+    assert lmk(P, 0, 2, 1, 4, 4, 1, P + 8, 8 * 1024, None) == 4   # 16-byte aligned workspace
     p = lib.gsa_prologue_vt
     assert p(P, 0, 2048, P, 0, 2048, P, 0, 2048, P, P, 128, 1, 4, 16, 128, 1, P, P, 100, None) == 2   # ldv % 64
     assert p(P, 0, 2048, None, 0, 2048, P, 0, 2048, P, P, 128, 1, 4, 16, 128, 1, P, P, 64, None) == 1

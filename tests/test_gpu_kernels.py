@@ -630,27 +630,22 @@ def test_dense_lane_masks_then_attention_equals_one_call(dev, causal_masks):
 
 
 def _lane_masks_expected(bits, T, Tkv):
-    """The dense attention's lane-mask words, stated from the bitmask alone:
-    word [b, g, kt, s] (s = 16c + r) has bit 32h + i set iff row 32g + i (< T)
-    selects key 64kt + 32c + 16(r // 8) + 8h + r % 8, the key that accumulator
-    r of lane (h, i) holds in half c of the S^T MFMA output."""
+    """The dense attention's mask operands, stated from the bitmask alone:
+    record [b, g, kt, l] (16 bytes, lane l = 32h + n) holds 32 e2m1 nibbles,
+    nibble i (bits 4i..4i+3, little-endian u32 words) 0x0 if row 32g + n (< T)
+    selects key 64kt + 32h + i and 0xF (-6.0) if not (rows past T select nothing)."""
     B = bits.shape[0]
     NT = (Tkv + 63) // 64
     rows_per_block = _abi.dense_block_rows(Tkv)                          # groups cover whole blocks
     G = (T + rows_per_block - 1) // rows_per_block * (rows_per_block // 32)
-    w = bits.cpu().numpy().view(np.uint32).astype(np.uint64)
-    w64 = w[..., 0::2] | (w[..., 1::2] << np.uint64(32))                  # [B, T, NT]
-    rows = np.zeros((B, G * 32, NT), np.uint64)
-    rows[:, :T] = w64
-    rows = rows.reshape(B, G, 32, NT)
-    s = np.arange(32)
-    out = np.zeros((B, G, NT, 32), np.uint64)
-    for h in range(2):
-        key = (32 * (s // 16) + 16 * ((s % 16) // 8) + 8 * h + s % 8).astype(np.uint64)
-        bit = (rows[..., None] >> key) & np.uint64(1)                      # [B, G, i, NT, s]
-        shift = (32 * h + np.arange(32)).astype(np.uint64)[None, None, :, None, None]
-        out |= np.bitwise_or.reduce(bit << shift, axis=2)
-    return out
+    w = bits.cpu().numpy().view(np.uint32)[..., :2 * NT].astype(np.uint64)   # [B, T, 2NT]
+    rows = np.zeros((B, G * 32, 2 * NT), np.uint64)
+    rows[:, :T] = w
+    rows = rows.reshape(B, G, 32, NT, 2).transpose(0, 1, 3, 4, 2)           # [B, G, NT, h, n]
+    sel = (rows[..., None] >> np.arange(32, dtype=np.uint64)) & np.uint64(1)   # [B, G, NT, h, n, 32]
+    nib = ((np.uint64(1) - sel) * np.uint64(15)).reshape(B, G, NT, 2, 32, 4, 8)
+    words = (nib << (np.uint64(4) * np.arange(8, dtype=np.uint64))).sum(-1)   # [B, G, NT, h, n, 4]
+    return words.reshape(B, G, NT, 64, 4).astype(np.uint32)
 
 
 @pytest.mark.parametrize("B,T,Tkv,density", [(2, 300, 300, 0.5), (1, 777, 1000, 0.1), (1, 64, 64, 0.9),
@@ -671,10 +666,10 @@ def test_dense_lane_masks_layout(dev, B, T, Tkv, density, causal):
     words = (sel.view(B, T, -1, 32).to(torch.int64) << torch.arange(32)).sum(-1)
     bits = words.to(torch.int32).contiguous().to(dev)
     want = _lane_masks_expected(bits, T, Tkv)
-    ws = torch.full((want.size * 8,), 0xA5, dtype=torch.uint8, device=dev)
+    ws = torch.full((want.size * 4,), 0xA5, dtype=torch.uint8, device=dev)
     _abi.dense_lane_masks(bits, Tkv, ws=ws, causal=causal)
     torch.cuda.synchronize()
-    got = ws.cpu().numpy().view(np.uint64).reshape(want.shape)
+    got = ws.cpu().numpy().view(np.uint32).reshape(want.shape)
     if not causal:
         assert np.array_equal(got, want)
         return
@@ -682,7 +677,7 @@ def test_dense_lane_masks_layout(dev, B, T, Tkv, density, causal):
     nt = np.minimum(want.shape[2], ((32 * np.arange(want.shape[1])) // rows + 1) * rows // 64)   # per group
     read = np.arange(want.shape[2])[None, :] < nt[:, None]                                     # [G, NT]
     assert np.array_equal(got[:, read], want[:, read])
-    assert np.all(got[:, ~read] == np.uint64(0xA5A5A5A5A5A5A5A5))
+    assert np.all(got[:, ~read] == np.uint32(0xA5A5A5A5))
 
 
 @pytest.mark.parametrize("causal", [False, True])
