@@ -445,14 +445,11 @@ def mask_words(Tkv: int) -> int:
     return 2 * ((Tkv + 63) // 64)
 
 
-DENSE_WIDE_TKV = 32768
-
-
 def dense_block_rows(Tkv: int) -> int:
-    """Query rows per block of gsa_dense_attn for Tkv keys: 256 (8 waves), 384
-    (12 waves) from DENSE_WIDE_TKV keys on.  The lane-mask workspace counts
-    whole blocks of this size (gsa_dense_attn_workspace_bytes)."""
-    return 384 if Tkv >= DENSE_WIDE_TKV else 256
+    """Query rows per block of gsa_dense_attn (8 waves of 32 rows), whatever the
+    key count.  The mask-operand workspace counts whole blocks of this size
+    (gsa_dense_attn_workspace_bytes)."""
+    return 256
 
 
 def prologue_vt(v, vg, k=None, cos=None, sin=None, k_out=None, vt=None, bits=None, Tkv=None, ws=None,

@@ -9,8 +9,8 @@
 // selection bits [B,T,W] uint32, W = 2*ceil(Tkv/64): bit j of row t set iff
 // key j is selected and valid for query t.
 //
-// Per block: one head, 256 query rows (8 waves of 32 rows; 384 rows in 12
-// waves from 32K keys on), 64-key tiles in LDS.  With
+// Per block: one head, 256 query rows (8 waves of 32 rows), 64-key tiles in
+// LDS.  With
 // v_mfma_f32_32x32x16_bf16 both products are computed transposed,
 //   S^T = K Q^T    (A = K tile from LDS, B = this wave's q, in registers)
 //   O^T = V^T P^T  (A = V^T tile from LDS, B = P in registers)
@@ -23,12 +23,9 @@
 
 namespace gsa {
 
-// Waves per dense-attention block (32 query rows each): 8 for keys shorter
-// than kDenseWideTkv, 12 from there on.  The lane-mask layout follows the
-// same rule (its 32-row groups are padded to whole blocks), so producer and
-// consumer agree from (T, Tkv) alone.
-constexpr int kDenseWideTkv = 32768;
-__host__ __device__ constexpr int dense_block_waves(int Tkv) { return Tkv >= kDenseWideTkv ? 12 : 8; }
+// Waves per dense-attention block (32 query rows each).  The mask-operand
+// layout pads its 32-row groups to whole blocks.
+constexpr int kDenseWaves = 8;
 constexpr int kDK = 64;          // keys per tile
 constexpr int kKS = 128 + 8;     // LDS row stride of prologue_vt's staging tile (elements)
 
@@ -218,15 +215,15 @@ __global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p,
 // ---------------------------------------------------------------------------
 // Dense masked attention (bf16)
 //
-// Block: W waves = 32W query rows of one head (wave w: rows 32w .. 32w+31):
-// 8 waves (two per SIMD) or 12 (three per SIMD), by dense_block_waves.  K
-// and V^T tiles and each wave's mask operands reach LDS by direct
+// Block: 8 waves = 256 query rows of one head (wave w: rows 32w .. 32w+31),
+// two waves per SIMD.  K and V^T tiles and each wave's mask operands reach
+// LDS by direct
 // global->LDS loads (16 B per lane; one instruction fills 1 KiB,
 // lane-linear), each through a pair of slots, K and V^T in padded layouts
 // (unit = 16 B = 8 bf16):
 //   K   tile: 64 keys x 17 units, unit 16 of a key is padding
 //   V^T tile: 128 rows x 9 units (64 keys), unit 8 of a row is padding
-//   mask:     W waves x 64 units (each lane's 16-byte B operand)
+//   mask:     8 waves x 64 units (each lane's 16-byte B operand)
 // The odd row strides make every MFMA operand read conflict-free (16 lanes
 // reading one unit of 16 different rows hit 16 different bank groups), and
 // each operand read is one base register plus an immediate offset.  Padding
@@ -242,12 +239,10 @@ __global__ __launch_bounds__(256) void prologue_vt_lane_mask_kernel(ProVtArgs p,
 // selected keys are the bf16 products alone, bit for bit.  No mask word
 // passes through scalar registers and the loop issues no scalar load.
 //
-// Tiles are pipelined (8 waves): S^T of tile t+1 is computed, one 32-key
-// half at a time, while tile t's row maxima are taken, then the tile's one
+// Tiles are pipelined: S^T of tile t+1 is computed, one 32-key half at a
+// time, while tile t's row maxima are taken, then the tile's one
 // online-softmax decision with the lazy reference (below), then O^T +=
 // V^T(t) P^T(t) half by half, so MFMA and VALU work of one wave overlap.
-// 12-wave blocks compute S^T(t) itself in that place (one S accumulator pair
-// per wave).
 // ---------------------------------------------------------------------------
 struct DenseArgs {
   const uint16_t* q; int64_t q_sb, q_st;
@@ -270,8 +265,8 @@ constexpr int kVU = 128 * kVRow;       // 1152 units: V^T tile
 constexpr int kDmaK = kKU / 64;        // 17 load instructions fill a K tile
 constexpr int kDmaV = kVU / 64;        // 18 fill a V^T tile
 constexpr int kMBase = 2 * (kKU + kVU);   // units: two K slots, two V^T slots, then the two mask slots
-// LDS of a W-wave block: the K and V^T slot pairs, then two mask slots of W KiB.
-__host__ __device__ constexpr size_t dense_lds_bytes(int W) { return (size_t)(kMBase + 2 * 64 * W) * 16; }
+// LDS of a block: the K and V^T slot pairs, then two mask slots of 8 KiB.
+constexpr size_t kDenseLds = (size_t)(kMBase + 2 * 64 * kDenseWaves) * 16;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef int intx8 __attribute__((ext_vector_type(8)));
@@ -318,31 +313,22 @@ __device__ __forceinline__ int swap_bits23(int i) { return (i & ~12) | ((i & 4) 
 
 template <int N> struct Int { static constexpr int value = N; };
 
-// Pipeline of one block (W waves = 32W query rows of one head), tile t = 64
+// Pipeline of one block (8 waves = 256 query rows of one head), tile t = 64
 // keys.  K tiles, V^T tiles and mask operands stream through separate pairs
-// of LDS slots (tile t in slot t&1).  With PP (ping-pong S), iteration t,
-// after one barrier:
+// of LDS slots (tile t in slot t&1).  Iteration t, after one barrier:
 //   loads  K(t+2) and its mask operands into K / mask slot t&1 (S(t) was
 //          computed last iteration) and V^T(t+1) into V slot (t+1)&1 (PV(t-1)
 //          is done);
 //   MFMA   S^T(t+1) from K slot (t+1)&1, interleaved with the row maxima of
 //          S(t) (VALU), then O^T += V^T(t) P^T(t) from V slot t&1.
 // So the S product of the next tile overlaps the softmax of this one, within
-// the wave, at the cost of a second S accumulator pair (64 VGPRs).  Without
-// PP, iteration t loads K(t+1), V^T(t+1) and the mask operands of t+1 into
-// slots (t+1)&1 and computes S^T(t), its softmax and PV(t) from slots t&1:
-// one S pair, so 12-wave blocks (three waves per SIMD) fit the register
-// file, and the overlap of MFMA and VALU work comes from the other waves of
-// the SIMD instead.  8 waves with PP is the faster form up to 16K keys, 12
-// without PP beyond (fewer tile loads per query row: at 65536 keys 17.1 ->
-// 15.9 ms, K and V^T no longer fit the last-level cache).  Every load is
-// issued one iteration before the barrier that publishes it; the loop is
-// unrolled by two so that slot offsets are constants.
-template <int W, bool PP>
-__global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, const u32x4* __restrict__ lm) {
-  extern __shared__ __align__(16) u32x4 dsm[];   // K slots 0, 1 (kKU units each), V^T slots 0, 1 (kVU), mask slots 0, 1 (64W)
-  constexpr int kDW = W;                          // waves per block
-  constexpr int kDQ = 32 * W;                     // query rows per block
+// the wave, at the cost of a second S accumulator pair (64 VGPRs).  Every
+// load is issued one iteration before the barrier that publishes it; the
+// loop is unrolled by two so that slot offsets are constants.
+__global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseArgs p, const u32x4* __restrict__ lm) {
+  extern __shared__ __align__(16) u32x4 dsm[];   // K slots 0, 1 (kKU units each), V^T slots 0, 1 (kVU), mask slots 0, 1 (512)
+  constexpr int kDW = kDenseWaves;                // waves per block
+  constexpr int kDQ = 32 * kDW;                   // query rows per block
   constexpr int kDmaKW = (kDmaK + kDW - 1) / kDW;   // K instructions per wave (wave w: i = kDW*n + w < 17)
   constexpr int kDmaVW = (kDmaV + kDW - 1) / kDW;   // V^T instructions per wave
   constexpr int kMSlot = 64 * kDW;                // units of one mask slot
@@ -419,10 +405,10 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
   auto issue_m = [&](int kt, int slot) {                       // tile kt's mask operands into mask slot `slot`
     load_lds16(mbase + (int64_t)kt * 1024, moff, mdst + (uint32_t)(slot * kDW * 1024));
   };
-  // prologue loads: K(0), K(1) (ping-pong only), V(0) and the mask operands of the same tiles
+  // prologue loads: K(0), K(1), V(0) and the mask operands of the same tiles
   issue_k(kbase, 0, nkt == 1);
   issue_m(0, 0);
-  if (PP && nkt > 1) {
+  if (nkt > 1) {
     issue_k(kbase + kstep, 1, nkt == 2);
     issue_m(1, 1);
   }
@@ -590,78 +576,45 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
     pv_half(vs, 1, pk1);
   };
 
-  if constexpr (PP) {
-    // S^T of tile kt in sc[kt & 1]: with the loop unrolled by two, each
-    // iteration writes the other pair, so no accumulator is copied
-    floatx16 sc[2][2];
-    {
-      const intx8 mop = mask_op(0);
-      sc[0][0] = s_half(0, 0, mop);
-      sc[0][1] = s_half(0, 1, mop);                 // S^T of tile 0
-    }
-    const char* ksrc = kbase + 2 * kstep;            // K tile kt+2
-    // one iteration; P = kt & 1
-    auto step = [&](int kt, auto par) {
-      constexpr int P = decltype(par)::value;
-      // this wave's loads of K(kt+1), its mask operands and V^T(kt) (issued
-      // last iteration) are done and its LDS reads have returned; the
-      // barrier publishes every wave's loads and frees K and mask slot P and
-      // V slot 1-P
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (kt + 2 < nkt) {
-        issue_k(ksrc, P, kt + 3 == nkt);
-        issue_m(kt + 2, P);
-      }
-      if (kt + 1 < nkt) issue_v(vsrc, 1 - P);
-      ksrc += kstep;
-      vsrc += kDK * 2;
-
-      // S^T(kt+1) || softmax(kt); stale on the last tile, unused
-      const intx8 mop = mask_op(1 - P);
-      sc[1 - P][0] = s_half(1 - P, 0, mop);
-      const float mx0 = max_half(sc[P][0]);
-      sc[1 - P][1] = s_half(1 - P, 1, mop);
-      const float mx1 = max_half(sc[P][1]);
-      softmax_pv(P, mx0, mx1, sc[P][0], sc[P][1]);
-    };
-    int t = 0;
-    for (; t + 1 < nkt; t += 2) {
-      step(t, Int<0>{});
-      step(t + 1, Int<1>{});
-    }
-    if (t < nkt) step(t, Int<0>{});
-  } else {
-    const char* ksrc = kbase + kstep;                // K tile kt+1
-    // one iteration; P = kt & 1
-    auto step = [&](int kt, auto par) {
-      constexpr int P = decltype(par)::value;
-      // this wave's loads of K(kt), V^T(kt) and its mask operands (issued
-      // last iteration) are done and its LDS reads have returned; the barrier
-      // publishes every wave's loads and frees slots 1-P (tile kt-1) for tile
-      // kt+1
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (kt + 1 < nkt) {
-        issue_k(ksrc, 1 - P, kt + 2 == nkt);
-        issue_v(vsrc, 1 - P);
-        issue_m(kt + 1, 1 - P);
-      }
-      ksrc += kstep;
-      vsrc += kDK * 2;
-
-      const intx8 mop = mask_op(P);
-      const floatx16 s0 = s_half(P, 0, mop);
-      const float mx0 = max_half(s0);
-      const floatx16 s1 = s_half(P, 1, mop);
-      const float mx1 = max_half(s1);
-      softmax_pv(P, mx0, mx1, s0, s1);
-    };
-    int t = 0;
-    for (; t + 1 < nkt; t += 2) {
-      step(t, Int<0>{});
-      step(t + 1, Int<1>{});
-    }
-    if (t < nkt) step(t, Int<0>{});
+  // S^T of tile kt in sc[kt & 1]: with the loop unrolled by two, each
+  // iteration writes the other pair, so no accumulator is copied
+  floatx16 sc[2][2];
+  {
+    const intx8 mop = mask_op(0);
+    sc[0][0] = s_half(0, 0, mop);
+    sc[0][1] = s_half(0, 1, mop);                 // S^T of tile 0
   }
+  const char* ksrc = kbase + 2 * kstep;            // K tile kt+2
+  // one iteration; P = kt & 1
+  auto step = [&](int kt, auto par) {
+    constexpr int P = decltype(par)::value;
+    // this wave's loads of K(kt+1), its mask operands and V^T(kt) (issued
+    // last iteration) are done and its LDS reads have returned; the
+    // barrier publishes every wave's loads and frees K and mask slot P and
+    // V slot 1-P
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + 2 < nkt) {
+      issue_k(ksrc, P, kt + 3 == nkt);
+      issue_m(kt + 2, P);
+    }
+    if (kt + 1 < nkt) issue_v(vsrc, 1 - P);
+    ksrc += kstep;
+    vsrc += kDK * 2;
+
+    // S^T(kt+1) || softmax(kt); stale on the last tile, unused
+    const intx8 mop = mask_op(1 - P);
+    sc[1 - P][0] = s_half(1 - P, 0, mop);
+    const float mx0 = max_half(sc[P][0]);
+    sc[1 - P][1] = s_half(1 - P, 1, mop);
+    const float mx1 = max_half(sc[P][1]);
+    softmax_pv(P, mx0, mx1, sc[P][0], sc[P][1]);
+  };
+  int t = 0;
+  for (; t + 1 < nkt; t += 2) {
+    step(t, Int<0>{});
+    step(t + 1, Int<1>{});
+  }
+  if (t < nkt) step(t, Int<0>{});
 
   // ---- epilogue: normalise, bf16, optional output gate ----
   l = sum_halves(l);
@@ -699,11 +652,10 @@ __global__ __launch_bounds__(64 * W, 1) void dense_attn_kernel(DenseArgs p, cons
 // ---------------------------------------------------------------------------
 using namespace gsa_host;
 
-// Per device and dense kernel (8 waves, 12 waves): its LDS limit has been
-// raised.  (A benign race: concurrent first calls both set the same
-// attribute.)
+// Per device: the dense kernel's LDS limit has been raised.  (A benign race:
+// concurrent first calls both set the same attribute.)
 static constexpr int kMaxDevices = 64;
-static bool g_dense_lds_set[kMaxDevices][2] = {};
+static bool g_dense_lds_set[kMaxDevices] = {};
 
 namespace {
 int prologue_vt_checks(const void* k, int64_t k_sb, int64_t k_st, const void* v, int64_t v_sb, int64_t v_st,
@@ -760,10 +712,10 @@ extern "C" int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st
 }
 
 namespace {
-// 32-row lane-mask groups of T query rows: whole blocks of the dense kernel
-// that runs for Tkv keys (8 groups per block, 12 from 32K keys on).
-int64_t dense_groups(int T, int Tkv) {
-  const int w = gsa::dense_block_waves(Tkv);
+// 32-row mask-operand groups of T query rows: whole 256-row blocks of the
+// dense kernel (8 groups per block).
+int64_t dense_groups(int T, int /*Tkv*/) {
+  constexpr int w = gsa::kDenseWaves;
   return (int64_t)((T + 32 * w - 1) / (32 * w)) * w;
 }
 }  // namespace
@@ -797,7 +749,7 @@ gsa::LaneMaskArgs lane_mask_args(const uint32_t* bits, int64_t b_sb, int64_t b_s
   const int NT = (Tkv + 63) / 64;
   const int G = (int)dense_groups(T, Tkv);
   const int nunits = B * G * ((NT + gsa::kLmTiles - 1) / gsa::kLmTiles);
-  const int block_rows = causal ? 32 * gsa::dense_block_waves(Tkv) : 0;
+  const int block_rows = causal ? 32 * gsa::kDenseWaves : 0;
   return gsa::LaneMaskArgs{bits, b_sb, b_st, T, G, NT, nunits, block_rows, static_cast<gsa::u32x4*>(ws)};
 }
 
@@ -863,7 +815,7 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
   // per-lane load offsets within a tile are 32-bit byte offsets
   if (k_st > (1 << 24) || (int64_t)ldv > (1 << 23)) return GSA_ERR_SHAPE;
-  const int W = gsa::dense_block_waves(Tkv);   // waves per block: 32W query rows
+  constexpr int W = gsa::kDenseWaves;         // waves per block: 32W query rows
   const int nqb = (T + 32 * W - 1) / (32 * W);
   const int64_t G = dense_groups(T, Tkv);      // 32-row groups, padded to whole blocks
   if ((int64_t)B * H * nqb > 0x7fffffffLL || B * G * NT > 0x7fffffffLL) return GSA_ERR_SHAPE;
@@ -891,19 +843,12 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                    B, T, Tkv, H, nqb, scale * gsa::kLog2e, flags | (causal ? gsa::kDenseCausal : 0)};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return GSA_ERR_SHAPE;
-  const bool wide = W == 12;
-  const void* fn = wide ? reinterpret_cast<const void*>(gsa::dense_attn_kernel<12, false>)
-                        : reinterpret_cast<const void*>(gsa::dense_attn_kernel<8, true>);
-  if (!g_dense_lds_set[dev][wide]) {   // more than the default 64 KiB of LDS per block
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsa::dense_lds_bytes(W));
+  if (!g_dense_lds_set[dev]) {   // more than the default 64 KiB of LDS per block
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gsa::dense_attn_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsa::kDenseLds);
     if (e != hipSuccess) return -static_cast<int>(e);
-    g_dense_lds_set[dev][wide] = true;
+    g_dense_lds_set[dev] = true;
   }
-  if (wide)
-    hipLaunchKernelGGL((gsa::dense_attn_kernel<12, false>), dim3(B * H * nqb), dim3(64 * 12), gsa::dense_lds_bytes(12),
-                       s, a, lm);
-  else
-    hipLaunchKernelGGL((gsa::dense_attn_kernel<8, true>), dim3(B * H * nqb), dim3(64 * 8), gsa::dense_lds_bytes(8),
-                       s, a, lm);
+  hipLaunchKernelGGL(gsa::dense_attn_kernel, dim3(B * H * nqb), dim3(64 * W), gsa::kDenseLds, s, a, lm);
   return launch_status();
 }

@@ -312,18 +312,20 @@ int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel
  * q, out, og [B,T,H,d]; k [B,Tkv,H,d] (RoPE'd); vt [B,H,d,ldv] as written by
  * gsa_prologue_vt (strides vt_sb, vt_sh per batch and head; rows of ldv).
  * causal != 0: key tiles after a query block's last row are skipped (the
- * selection must then be causal; a block holds 256 query rows, 384 when
- * Tkv >= 32768).  ws: caller-provided device workspace
- * of at least gsa_dense_attn_workspace_bytes(B, T, Tkv) bytes (8-byte
- * aligned), overwritten by each call -- or, with GSA_ATTN_MASKS_READY, the
- * lane masks gsa_dense_lane_masks wrote there for the same bits, B, T, Tkv
- * and causal (then bits is not read).  bf16 only; d == 128, 1 <= H <= 64.
+ * selection must then be causal; a block holds 256 query rows).
+ * ws: caller-provided device workspace of at least
+ * gsa_dense_attn_workspace_bytes(B, T, Tkv) bytes (16-byte aligned; 1 KiB
+ * of mask operands per 32 query rows and 64 keys), overwritten by each call
+ * -- or, with GSA_ATTN_MASKS_READY, the mask operands gsa_dense_lane_masks
+ * wrote there for the same bits, B, T, Tkv and causal (then bits is not
+ * read).  bf16 only; d == 128, 1 <= H <= 64.
  */
 size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
 
 /*
  * The first step of gsa_dense_attn on its own: the selection bitmask ->
- * per-lane masks of the attention kernel's score slots, into ws (same size
+ * the attention kernel's mask operands (4 bits per query row and key: the
+ * e2m1 operand of the MFMA that starts each score tile), into ws (same size
  * and alignment as gsa_dense_attn's workspace).  Lets a caller build them
  * on another stream, beside other work, and pass GSA_ATTN_MASKS_READY.
  * causal != 0: only the key tiles a causal gsa_dense_attn reads (up to the

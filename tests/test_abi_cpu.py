@@ -218,11 +218,10 @@ def test_dense_path_validation(lib):
     assert lib.gsa_dense_attn_workspace_bytes(1, 4, 4) == 8 * 1024
     assert lib.gsa_dense_attn_workspace_bytes(2, 100, 130) == 2 * 8 * 3 * 1024
     assert lib.gsa_dense_attn_workspace_bytes(1, 257, 64) == 16 * 1024
-    # from 32768 keys on the blocks hold 384 rows (12 groups)
-    assert _abi.dense_block_rows(32767) == 256 and _abi.dense_block_rows(32768) == 384
-    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 32767) == 8 * 512 * 1024
-    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 32768) == 12 * 512 * 1024
-    assert lib.gsa_dense_attn_workspace_bytes(2, 385, 40000) == 2 * 24 * 625 * 1024
+    # 256-row blocks at every key count
+    assert _abi.dense_block_rows(32767) == 256 and _abi.dense_block_rows(65536) == 256
+    assert lib.gsa_dense_attn_workspace_bytes(1, 4, 32768) == 8 * 512 * 1024
+    assert lib.gsa_dense_attn_workspace_bytes(2, 385, 40000) == 2 * 16 * 625 * 1024
     assert call(bits=None) == 1
     assert call(ws=None) == 1
     assert call(wsb=8 * 1024 - 1) == 2            # workspace too small

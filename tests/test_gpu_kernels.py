@@ -560,11 +560,11 @@ def _vt_of(v, dev):
 @pytest.mark.parametrize("B,T,Tkv,H,k,causal", [(1, 800, 33000, 2, 300, False), (1, 800, 33000, 2, 300, True),
                                                 (1, 385, 32768, 1, 64, False), (2, 400, 32768, 3, 96, True)])
 def test_dense_attention_long_keys_vs_oracle(dev, B, T, Tkv, H, k, causal):
-    """From 32768 keys on gsa_dense_attn runs 12-wave (384-row) blocks: ragged
-    query blocks (T = 2*384 + 32, 384 + 1), a ragged last key tile (33000 =
-    515*64 + 40), causal and non-causal selections, RoPE(q) and the output gate,
-    against the float64 oracle with the bound of the short-key test; a batch of
-    two sequences checks the per-sequence offsets."""
+    """Long key ranges (more than 512 tiles per row): ragged query blocks (T =
+    3*256 + 32, 256 + 129), a ragged last key tile (33000 = 515*64 + 40), causal
+    and non-causal selections, RoPE(q) and the output gate, against the float64
+    oracle with the bound of the short-key test; a batch of two sequences
+    checks the per-sequence offsets."""
     _log(f"dense_attn long keys B={B} T={T} Tkv={Tkv} H={H} k={k} causal={causal}")
     q, kk, v, og, ia, cnt = _long_keys_case(T, Tkv, H, k, seed=T + Tkv, causal=causal, B=B)
     cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
@@ -583,14 +583,13 @@ def test_dense_attention_long_keys_vs_oracle(dev, B, T, Tkv, H, k, causal):
     assert rel < 5e-3
 
 
-def test_dense_attention_block_shapes_bit_identical(dev):
-    """The 12-wave kernel (32768 keys) and the 8-wave one (the first 32000 of
-    the same keys) on a selection that only uses keys below 32000: every row
-    runs the same per-wave arithmetic in both (the extra tiles are fully
-    masked and add exact zeros), so the outputs agree bit for bit."""
+def test_dense_attention_masked_tiles_add_nothing(dev):
+    """32768 keys against the first 32000 of the same keys, on a selection that
+    only uses keys below 32000: the 12 extra tiles of every row are fully
+    masked (their mask products start the scores near -8e36, so their p are
+    exact zeros), so the outputs agree bit for bit."""
     T, H, k = 1000, 2, 256
-    _log(f"dense_attn 12-wave vs 8-wave blocks T={T} H={H} k={k}")
-    assert _abi.dense_block_rows(32768) == 384 and _abi.dense_block_rows(32000) == 256
+    _log(f"dense_attn masked tiles T={T} H={H} k={k}")
     q, kk, v, og, ia, cnt = _long_keys_case(T, 32768, H, k, seed=7, causal=False, key_limit=32000)
     cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
     qd, ogd, cosd, sind, iad, cntd = (t.to(dev) for t in (q, og, cos, sin, ia, cnt))
@@ -650,7 +649,7 @@ def _lane_masks_expected(bits, T, Tkv):
 
 @pytest.mark.parametrize("B,T,Tkv,density", [(2, 300, 300, 0.5), (1, 777, 1000, 0.1), (1, 64, 64, 0.9),
                                              (3, 520, 130, 0.03),
-                                             # 384-row blocks (12 groups) from 32768 keys on
+                                             # more than 512 key tiles
                                              (1, 400, 32800, 0.01), (2, 390, 32800, 0.01)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_dense_lane_masks_layout(dev, B, T, Tkv, density, causal):
