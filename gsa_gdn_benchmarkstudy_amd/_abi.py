@@ -281,8 +281,18 @@ def indexer_select_noalloc(q_idx, k_idx, w, bias32, scale: float, k_eff: int, bi
     lib = load()
     _need_cuda(q_idx, k_idx, w, bias32, bits, idx, cnt)
     B, T, Hi, di = q_idx.shape
-    _expect(tuple(bits.shape) == (B, T, mask_words(T)) and bits.is_contiguous(), "bits: contiguous [B,T,W]")
+    _expect(tuple(k_idx.shape) == (B, T, di), f"k_idx {tuple(k_idx.shape)} != {(B, T, di)}")
+    _expect(tuple(w.shape) == (B, T, Hi), f"w {tuple(w.shape)} != {(B, T, Hi)}")
+    _expect(bias32.dtype == torch.float32 and bias32.numel() == Hi and bias32.is_contiguous(), "bias: fp32 [Hi]")
+    _expect(k_idx.dtype == q_idx.dtype == w.dtype, "q_idx, k_idx, w must share a dtype")
+    _expect(tuple(bits.shape) == (B, T, mask_words(T)) and bits.is_contiguous() and bits.dtype == torch.int32,
+            "bits: contiguous int32 [B,T,W]")
     _expect((idx is None) == (cnt is None), "idx and cnt go together")
+    if idx is not None:
+        _expect(tuple(idx.shape) == (B, T, int(k_eff)) and idx.dtype == torch.int32 and idx.is_contiguous(),
+                "idx: contiguous int32 [B,T,k_eff]")
+        _expect(tuple(cnt.shape) == (B, T) and cnt.dtype == torch.int32 and cnt.is_contiguous(),
+                "cnt: contiguous int32 [B,T]")
     qs, ks, wst = _rows(q_idx, Hi * di), _rows(k_idx, di), _rows(w, Hi)
     st = lib.gsa_indexer_select_noalloc(_ptr(q_idx), *qs, _ptr(k_idx), *ks, _ptr(w), *wst, _ptr(bias32),
                                         float(scale), B, T, Hi, di, int(k_eff), dtype_code(q_idx.dtype),

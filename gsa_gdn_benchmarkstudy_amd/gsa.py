@@ -464,6 +464,11 @@ class GatedSparseAttention(nn.Module):
         v.update(self.project_main(x))
         return v
 
+    # Longest sequence the fused indexer + top-k takes (key positions and
+    # sample counts are 16-bit there); longer ones go through the full score
+    # matrix (gsa_indexer_scores, 4*B*T*T bytes) and the standalone selector.
+    FUSED_SELECT_MAX_T = 65536
+
     def select(self, views, T: int, indices: bool = True):
         """Fused indexer + top-k on the current stream -> (bits, idx, count).
 
@@ -474,6 +479,14 @@ class GatedSparseAttention(nn.Module):
         bias = self._idx_bias32
         if bias is None or bias.device != views["iq"].device:
             bias = self._idx_bias32 = self.indexer.idx_bias.detach().float().contiguous()
+        if T > self.FUSED_SELECT_MAX_T:
+            # the reference's own route (gsa_opt.py:660-677): the fp32 score
+            # matrix, then the exact selection in index order
+            scores = _abi.indexer_scores(views["iq"], views["ik"], views["iw"], bias, self.indexer.scale)
+            idx, cnt, _ = sel.select_ascending(scores)
+            del scores
+            bits = _abi.selection_mask(idx, T, count=cnt)
+            return (bits, idx, cnt) if indices else (bits, None, None)
         if sel.adaptive():
             bits, idx, cnt, k_rows, _ = _abi.indexer_select_adaptive(
                 views["iq"], views["ik"], views["iw"], bias, self.indexer.scale, sel.k_base, sel.k_min,

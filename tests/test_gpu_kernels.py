@@ -628,6 +628,25 @@ def test_dense_lane_masks_then_attention_equals_one_call(dev, causal_masks):
     assert torch.equal(one.cpu(), two.cpu())
 
 
+def test_causal_masks_refused_by_a_non_causal_call(dev):
+    """Mask operands built for a causal attention leave the tiles past each
+    query block unwritten: dense_attn refuses them for a non-causal call
+    (before any launch) and takes them for a causal one."""
+    B, T, H, k = 1, 300, 2, 64
+    q, kk, v, og, ia, cnt = _dense_case(B, T, H, k, seed=17)
+    qd, kd = q.to(dev), kk.to(dev)
+    vt = torch.zeros(B, H, 128, _abi.vt_len(T), dtype=torch.bfloat16, device=dev)
+    vt[..., :T] = v.to(dev).permute(0, 2, 3, 1)
+    bits = _abi.selection_mask(ia.to(dev), T, count=cnt.to(dev))
+    ws = _abi.dense_lane_masks(bits, T, causal=True)
+    with pytest.raises(ValueError):
+        _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, causal=False, ws=ws, masks_ready=True)
+    a = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, causal=True, ws=ws, masks_ready=True)
+    b = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
 def _lane_masks_expected(bits, T, Tkv):
     """The dense attention's mask operands, stated from the bitmask alone:
     record [b, g, kt, l] (16 bytes, lane l = 32h + n) holds 32 e2m1 nibbles,

@@ -234,3 +234,25 @@ def test_indexer_overlap_modes_identical(dev):
             m(x)
     for y in outs[1:]:
         assert torch.equal(y, outs[0])
+
+
+@pytest.mark.parametrize("impl", ["dense", "gather"])
+@pytest.mark.parametrize("mode", ["fixed", "variance"])
+def test_long_sequence_select_route_equals_fused(dev, impl, mode):
+    """Sequences longer than the fused indexer + top-k takes (65536 tokens) go
+    through the fp32 score matrix and the standalone selector.  That route,
+    forced here by lowering the limit to 200 tokens, computes the same
+    selection (same scores, same exact top-k) and so the same output bit for
+    bit as the fused one, in both attention kernels and both selector modes."""
+    cfg = orc.GSAConfig(hidden_size=512, num_heads=4, k_max=96, k_base=64, k_min=16)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=41), torch.bfloat16)
+    x = orc.synthetic_input(2, 300, cfg.hidden_size, seed=42).to(torch.bfloat16).to(dev)
+    m = _model(cfg, sd, dev, torch.bfloat16, impl=impl)
+    m.topk_selector.mode = mode
+    with torch.no_grad():
+        fused = m(x)
+        assert m.FUSED_SELECT_MAX_T == 65536
+        m.FUSED_SELECT_MAX_T = 200
+        routed = m(x)
+    torch.cuda.synchronize()
+    assert torch.equal(routed, fused)

@@ -5,7 +5,7 @@ k_max=4096, weights N(0, 0.02), gate biases 0.5, indexer biases 0, bf16):
   * B=1, T=16384 -- the bench's headline workload; dense and gather attention;
   * B=4, T=8192, sequence b scaled by sigma_b ~ U(0.5, 2); fixed k and the
     variance-based per-row k;
-  * B=1, T=65536 -- dense attention.
+  * B=1, T=65536 -- dense and gather attention.
 
 The GPU runs the whole layer forward.  The oracle then projects the keys
 (k, v, k_idx) of every row and the queries only for 32-row blocks spread over
@@ -213,9 +213,10 @@ def test_layer_B4_T8192_sigma_variance_k(dev):
 
 
 @pytest.mark.timeout(900)
-def test_layer_T65536_long_context(dev):
-    """B=1, T=65536 on the dense path: rows at the start, around k, the middle and the end."""
-    _log("layer T=65536 impl=dense")
+@pytest.mark.parametrize("impl", ["dense", "gather"])
+def test_layer_T65536_long_context(dev, impl):
+    """B=1, T=65536, both attention kernels: rows at the start, around k, the middle and the end."""
+    _log(f"layer T=65536 impl={impl}")
     sd, x = _inputs(1, 65536)
-    run = GpuRun(_model(sd, dev, "dense"), x, (0, 2048, 32768, 65504))
-    _check_layer(sd, x, run, "dense")
+    run = GpuRun(_model(sd, dev, impl), x, (0, 2048, 32768, 65504))
+    _check_layer(sd, x, run, impl)

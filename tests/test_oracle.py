@@ -242,6 +242,49 @@ def test_adaptive_k_formula():
     assert k[0].tolist() == exp.astype(int).tolist()
 
 
+def _adaptive_k_numpy(s, k_base, k_min, k_max, per_sequence_mean=False):
+    """The notebook rule (gsa_explained.ipynb:577-592) evaluated row by row in
+    float64: population variance of each row's finite scores, the mean of those
+    variances over every (batch, row) -- or, for the planted mutant, over each
+    sequence's rows only -- and k = clip(floor(k_base * avg / var), k_min, k_max)
+    with both variances floored at 1e-6."""
+    a = s.numpy().astype(np.float64)
+    B, T, _ = a.shape
+    var = np.zeros((B, T))
+    for b in range(B):
+        for t in range(T):
+            row = a[b, t][np.isfinite(a[b, t])]
+            var[b, t] = np.var(row) if row.size else 0.0
+    avg = var.mean(axis=1, keepdims=True) if per_sequence_mean else np.full((B, 1), var.mean())
+    avg = np.maximum(avg, 1e-6)
+    return np.clip(np.floor(k_base * avg / np.maximum(var, 1e-6)), k_min, k_max).astype(np.int64)
+
+
+def test_adaptive_k_mean_over_all_sequences():
+    """B=2 sequences whose scores spread differently (uniform on [0,1) and on
+    [0,3)): the oracle's k equals the float64 row-by-row evaluation with the
+    variance mean taken over all B*T rows, and a per-sequence mean -- a
+    plausible misreading of the notebook's variance.mean() -- gives other k
+    on most rows, so the check tells the two apart."""
+    T, k_base, k_min, k_max = 40, 16, 4, 64
+    g = torch.Generator().manual_seed(77)
+    s = torch.rand(2, T, T, generator=g, dtype=torch.float64)
+    s[1] *= 3.0
+    s = s.masked_fill(torch.triu(torch.ones(T, T, dtype=torch.bool), 1), float("-inf"))
+    got = orc.adaptive_k(s, k_base, k_min, k_max).numpy()
+    want = _adaptive_k_numpy(s, k_base, k_min, k_max)
+    assert np.array_equal(got, want)
+    mutant = _adaptive_k_numpy(s, k_base, k_min, k_max, per_sequence_mean=True)
+    assert (mutant != want).mean() > 0.5
+    # the variance itself against numpy, every row
+    var = orc.row_variance(s).numpy()
+    for b in range(2):
+        for t in range(T):
+            assert abs(var[b, t] - np.var(s[b, t, :t + 1].numpy())) <= 1e-12
+    # the spread of sequence 1 is 9x that of sequence 0: its rows get smaller k
+    assert want[1, 4:].mean() < want[0, 4:].mean()
+
+
 # ---------------------------------------------------------------------------
 # Sparse attention
 # ---------------------------------------------------------------------------

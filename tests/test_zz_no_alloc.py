@@ -54,3 +54,35 @@ def test_noalloc_select_rejects_sizes_past_its_scratch(dev):
                                         bias.to(dev).data_ptr(), 0.125, 8193, 16, 4, 64, 8, _abi.DTYPE_BF16,
                                         bits.data_ptr(), 32, 2, None, None, None)
     assert st == 7
+
+
+def test_noalloc_wrapper_checks_outputs_before_any_launch(dev):
+    """The Python binding refuses outputs the kernels would overrun (idx/cnt of
+    the wrong shape or dtype, bits of a narrower dtype) and inputs that
+    gsa_indexer_select's binding refuses, before the library is called."""
+    B, T, k = 1, 100, 16
+    buf, bias = _inputs(B, T, torch.bfloat16, seed=3)
+    bd = buf.to(dev)
+    q, kk, w = bd[..., :256].view(B, T, 4, 64), bd[..., 256:320], bd[..., 320:324]
+    b32 = bias.to(dev)
+    W = _abi.mask_words(T)
+    bits = torch.zeros(B, T, W, device=dev, dtype=torch.int32)
+    idx = torch.zeros(B, T, k, device=dev, dtype=torch.int32)
+    cnt = torch.zeros(B, T, device=dev, dtype=torch.int32)
+    bad = [
+        dict(idx=torch.zeros(B, T, k - 1, device=dev, dtype=torch.int32)),       # undersized idx
+        dict(cnt=torch.zeros(B, T - 1, device=dev, dtype=torch.int32)),          # undersized cnt
+        dict(idx=torch.zeros(B, T, k, device=dev, dtype=torch.int64)),           # idx dtype
+        dict(bits=torch.zeros(B, T, W, device=dev, dtype=torch.int16)),          # narrower bits
+        dict(w=bd[..., 320:323]),                                                # w [B,T,3]
+        dict(b32=b32.to(torch.bfloat16)),                                        # bias dtype
+        dict(kk=bd[..., 256:320].float()),                                       # mixed dtypes
+    ]
+    for over in bad:
+        a = dict(q=q, kk=kk, w=w, b32=b32, bits=bits, idx=idx, cnt=cnt)
+        a.update(over)
+        with pytest.raises(ValueError):
+            _abi.indexer_select_noalloc(a["q"], a["kk"], a["w"], a["b32"], 0.125, k, a["bits"], a["idx"], a["cnt"])
+    _abi.indexer_select_noalloc(q, kk, w, b32, 0.125, k, bits, idx, cnt)
+    torch.cuda.synchronize()
+    assert int(cnt[0, -1]) == k
