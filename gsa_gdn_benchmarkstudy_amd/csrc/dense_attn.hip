@@ -265,8 +265,17 @@ constexpr int kVU = 128 * kVRow;       // 1152 units: V^T tile
 constexpr int kDmaK = kKU / 64;        // 17 load instructions fill a K tile
 constexpr int kDmaV = kVU / 64;        // 18 fill a V^T tile
 constexpr int kMBase = 2 * (kKU + kVU);   // units: two K slots, two V^T slots, then the two mask slots
-// LDS of a block: the K and V^T slot pairs, then two mask slots of 8 KiB.
-constexpr size_t kDenseLds = (size_t)(kMBase + 2 * 64 * kDenseWaves) * 16;
+constexpr int kXBase = kMBase + 2 * 64 * kDenseWaves;   // units: the waves' 8 KiB staging tiles
+// LDS of a block: the K and V^T slot pairs, two mask slots of 8 KiB, and one
+// 8 KiB staging tile per wave (q, the RoPE tables and the output gate on
+// the way in, the output on the way out).
+constexpr size_t kDenseLds = (size_t)(kXBase + 512 * kDenseWaves) * 16;
+
+// Staging tile: 32 rows x 256 bytes (16 chunks of 16 bytes); chunk c of row
+// r sits at chunk slot c ^ (r & 15), so that a row load (4 rows x 256 bytes
+// per instruction, lane-linear) and an operand read (one chunk of 32 rows)
+// are both conflict-free.  Unit offset of (row, chunk) within the tile:
+__device__ __forceinline__ int xs_unit(int row, int chunk) { return row * 16 + (chunk ^ (row & 15)); }
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef int intx8 __attribute__((ext_vector_type(8)));
@@ -345,8 +354,6 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
   const int qb = p.nqb - 1 - r2 / p.H;
   const int hd = r2 % p.H;
   const int q0 = qb * kDQ;
-  const int qrow = q0 + 32 * w + i32;
-  const int qr = min(qrow, p.T - 1);
 
   const int last_key = (p.flags & kDenseCausal) ? min(p.Tkv - 1, q0 + kDQ - 1) : p.Tkv - 1;
   const int nkt = last_key / kDK + 1;
@@ -405,7 +412,31 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
   auto issue_m = [&](int kt, int slot) {                       // tile kt's mask operands into mask slot `slot`
     load_lds16(mbase + (int64_t)kt * 1024, moff, mdst + (uint32_t)(slot * kDW * 1024));
   };
-  // prologue loads: K(0), K(1), V(0) and the mask operands of the same tiles
+  // ---- the wave's staging tile (rows q0 + 32w .. +31, clamped to T-1; 256
+  // bytes each at a column offset): 8 loads of 4 rows x 256 bytes, each
+  // lane's 16 bytes placed by the tile's chunk swizzle.  Loading whole rows
+  // per instruction keeps every load to 8 cache lines; a lane-per-row load
+  // of the same data touches 32 lines per instruction, and a block's
+  // prologue then waited several microseconds for its q, cos and sin.
+  const int rbase = min(q0 + 32 * wu, p.T - 1);
+  const uint32_t xdst = lds0 + (uint32_t)((kXBase + wu * 512) * 16);
+  const u32x4* xt = dsm + kXBase + wu * 512;
+  auto stage = [&](const uint16_t* base, int64_t row_st) {   // base: element (rbase, column offset)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * j + (lane >> 4);
+      const uint32_t roff = (uint32_t)(min(q0 + 32 * wu + r, p.T - 1) - rbase);
+      load_lds16(base, roff * (uint32_t)(row_st * 2) + (uint32_t)(((lane & 15) ^ (r & 15)) * 16),
+                 xdst + (uint32_t)(j * 1024));
+    }
+  };
+
+  // ---- q: B operand of S^T; lane supplies d = 16s + 8h .. +7 of its row ----
+  stage(p.q + b * p.q_sb + (int64_t)rbase * p.q_st + hd * 128, p.q_st);
+  // prologue loads: K(0), K(1), V(0) and the mask operands of the same
+  // tiles, issued after q's so that q does not wait behind them: every wave
+  // issues at least 5 of them (2 K, 1 mask, 2 V^T), so vmcnt(5) leaves only
+  // tile loads in flight
   issue_k(kbase, 0, nkt == 1);
   issue_m(0, 0);
   if (nkt > 1) {
@@ -413,21 +444,35 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
     issue_m(1, 1);
   }
   issue_v(vtb, 0);
-
-  // ---- q: B operand of S^T; lane supplies d = 16s + 8h .. +7 of its row ----
+  asm volatile("s_waitcnt vmcnt(5)" ::: "memory");   // this wave's q rows have landed
   u32x4 qraw[8];
-  const uint16_t* qp = p.q + b * p.q_sb + (int64_t)qr * p.q_st + hd * 128;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) qraw[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * h);
+  for (int s = 0; s < 8; ++s) qraw[s] = xt[xs_unit(i32, 2 * s + h)];
   if (p.flags & GSA_ATTN_ROPE_Q) {
+    // the cos and sin rows through the same tile, after the q reads returned
+    u32x4 craw[8], sraw[8];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    stage(p.cos + (int64_t)rbase * p.cs_st, p.cs_st);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < 8; ++s) craw[s] = xt[xs_unit(i32, 2 * s + h)];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    stage(p.sin + (int64_t)rbase * p.cs_st, p.cs_st);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < 8; ++s) sraw[s] = xt[xs_unit(i32, 2 * s + h)];
+    auto unpack8 = [](const u32x4& v, float (&x)[8]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { x[2 * i] = bf16lo(v[i]); x[2 * i + 1] = bf16hi(v[i]); }
+    };
     // rotate_half partner of d (d < 64: -x[d+64]; else x[d-64]) is register s^4
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       float c0[8], s0[8], c1[8], s1[8];
-      load8(p.cos + (int64_t)qr * p.cs_st + 16 * s + 8 * h, c0);
-      load8(p.sin + (int64_t)qr * p.cs_st + 16 * s + 8 * h, s0);
-      load8(p.cos + (int64_t)qr * p.cs_st + 16 * (s + 4) + 8 * h, c1);
-      load8(p.sin + (int64_t)qr * p.cs_st + 16 * (s + 4) + 8 * h, s1);
+      unpack8(craw[s], c0);
+      unpack8(sraw[s], s0);
+      unpack8(craw[s + 4], c1);
+      unpack8(sraw[s + 4], s1);
       float lo[8], hi[8], ylo[8], yhi[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -600,6 +645,9 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
     if (kt + 1 < nkt) issue_v(vsrc, 1 - P);
     ksrc += kstep;
     vsrc += kDK * 2;
+    // the output-gate rows into the staging tile (free since the q and RoPE
+    // reads before the first barrier), awaited at the next barrier
+    if (kt == 0 && (p.flags & GSA_ATTN_OUT_GATE)) stage(p.og + b * p.o_sb + (int64_t)rbase * p.o_st + hd * 128, p.o_st);
 
     // S^T(kt+1) || softmax(kt); stale on the last tile, unused
     const intx8 mop = mask_op(1 - P);
@@ -622,26 +670,36 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
   // (the product is within 1.5 fp32 ulp of the quotient before the bf16
   // rounding); a row without any selected key (l = 0) gives 0
   const float inv_l = l > 0.f ? 1.f / l : 0.f;
-  if (qrow < p.T) {
-    uint16_t* op = p.out + b * p.out_sb + (int64_t)qrow * p.out_st + hd * 128;
-    const uint16_t* gp = (p.flags & GSA_ATTN_OUT_GATE) ? p.og + b * p.o_sb + (int64_t)qrow * p.o_st + hd * 128
-                                                       : nullptr;
+  // O / l (and the gate) in the accumulator layout, written into the
+  // staging tile at the gate values' places; then each row's 256 bytes go
+  // out 4 rows per store instruction.  (With a single tile the gate loads
+  // were issued in iteration 0 and may still be in flight.)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  char* const xb = reinterpret_cast<char*>(dsm + kXBase + wu * 512);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int d0 = 32 * dt + 8 * r4 + 4 * h;
-        float r[4];
+    for (int r4 = 0; r4 < 4; ++r4) {
+      uint2* const xp = reinterpret_cast<uint2*>(xb + xs_unit(i32, 4 * dt + r4) * 16 + 8 * h);
+      float r[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = round_bf16(o[dt][4 * r4 + e] * inv_l);
-        if (gp) {
-          const uint2 gw = *reinterpret_cast<const uint2*>(gp + d0);
-          const float gl[4] = {bf16lo(gw.x), bf16hi(gw.x), bf16lo(gw.y), bf16hi(gw.y)};
+      for (int e = 0; e < 4; ++e) r[e] = round_bf16(o[dt][4 * r4 + e] * inv_l);
+      if (p.flags & GSA_ATTN_OUT_GATE) {
+        const uint2 gw = *xp;
+        const float gl[4] = {bf16lo(gw.x), bf16hi(gw.x), bf16lo(gw.y), bf16hi(gw.y)};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) r[e] = round_bf16(r[e] * round_bf16(sigmoidf_fast(gl[e])));
-        }
-        *reinterpret_cast<uint2*>(op + d0) = uint2{pack_bf16(r[0], r[1]), pack_bf16(r[2], r[3])};
+        for (int e = 0; e < 4; ++e) r[e] = round_bf16(r[e] * round_bf16(sigmoidf_fast(gl[e])));
       }
+      *xp = uint2{pack_bf16(r[0], r[1]), pack_bf16(r[2], r[3])};
+    }
+  asm volatile("" ::: "memory");
+  uint16_t* const ob = p.out + b * p.out_sb + hd * 128;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = 4 * j + (lane >> 4), row = q0 + 32 * wu + r;
+    const u32x4 v = xt[r * 16 + (lane & 15)];
+    if (row < p.T)
+      *reinterpret_cast<u32x4*>(ob + (int64_t)row * p.out_st + (((lane & 15) ^ (r & 15)) * 8)) = v;
   }
 }
 
@@ -815,6 +873,10 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
   if (ws_bytes < gsa_dense_attn_workspace_bytes(B, T, Tkv)) return GSA_ERR_SHAPE;
   // per-lane load offsets within a tile are 32-bit byte offsets
   if (k_st > (1 << 24) || (int64_t)ldv > (1 << 23)) return GSA_ERR_SHAPE;
+  // the staging tiles' row offsets (32 rows) are 32-bit byte offsets
+  if (q_st > (1 << 24) || out_st > (1 << 24) || ((flags & GSA_ATTN_OUT_GATE) && o_st > (1 << 24)) ||
+      ((flags & GSA_ATTN_ROPE_Q) && cs_st > (1 << 24)))
+    return GSA_ERR_SHAPE;
   constexpr int W = gsa::kDenseWaves;         // waves per block: 32W query rows
   const int nqb = (T + 32 * W - 1) / (32 * W);
   const int64_t G = dense_groups(T, Tkv);      // 32-row groups, padded to whole blocks
