@@ -68,9 +68,25 @@ def indexer_flops(B, T):
     return 2 * B * HI * DI * T * (T + 1) // 2
 
 
+KERNEL_SOURCES = {"gsa_dense_attn": "dense_attn.hip", "gsa_indexer_select": "indexer.hip",
+                  "gsa_sparse_attn": "sparse_attn.hip"}
+
+
+def source_digest(kernel):
+    """First 12 hex digits of the SHA-256 of the HIP source file that holds `kernel`."""
+    import hashlib
+    path = os.path.join(ROOT, "gsa_gdn_benchmarkstudy_amd", "csrc", KERNEL_SOURCES[kernel])
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:12]
+
+
 def profiled_traffic(kernel, config):
-    """HBM-side bytes per launch of `kernel` at `config`, from the committed rocprofv3
-    PMC summaries (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration), or None."""
+    """HBM-side bytes per launch of `kernel` at `config` from the committed rocprofv3
+    PMC summaries (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration):
+    {"bytes", "source", "kernel_source", "measured_on_source", "source_matches"}, or
+    None.  A summary line reads `traffic_bytes <kernel> <config> <bytes> [src=<file>@<sha12>]`;
+    `source_matches` says whether the kernel's source file still has the digest that
+    the counters were taken on (False: the figure predates a kernel change)."""
     pdir = os.path.join(ROOT, "profiles")
     try:
         names = sorted(f for f in os.listdir(pdir) if f.endswith("_pmc.md"))
@@ -79,8 +95,11 @@ def profiled_traffic(kernel, config):
     for name in names:
         for line in open(os.path.join(pdir, name)):
             f = line.split()
-            if len(f) == 4 and f[0] == "traffic_bytes" and f[1] == kernel and f[2] == config:
-                return int(f[3])
+            if len(f) in (4, 5) and f[0] == "traffic_bytes" and f[1] == kernel and f[2] == config:
+                src = f[4][4:] if len(f) == 5 and f[4].startswith("src=") else None
+                cur = f"{KERNEL_SOURCES[kernel]}@{source_digest(kernel)}"
+                return {"bytes": int(f[3]), "source": f"profiles/{name}", "kernel_source": cur,
+                        "measured_on_source": src, "source_matches": src == cur}
     return None
 
 
@@ -316,12 +335,14 @@ def main():
     gather_gbs = abytes / (gather_ms * 1e-3) / 1e9
     aflops = 4 * P * H * DH                     # useful (selected-pair) QK and PV flops
     fidx = indexer_flops(B, T)
+    i_prof = profiled_traffic("gsa_indexer_select", args.config)
     idx_tflops = fidx / (idx_ms * 1e-3) / 1e12
-    g_traffic = profiled_traffic("gsa_sparse_attn", args.config)
+    g_prof = profiled_traffic("gsa_sparse_attn", args.config)
+    g_traffic = None if g_prof is None else g_prof["bytes"]
     g_rate = None if g_traffic is None else g_traffic / (gather_ms * 1e-3) / 1e9
     gather_roof = {"kernel": "gsa_sparse_attn", "bound": "hbm", "achieved": g_rate, "peak": HBM_PEAK_GBS,
                    "unit": "GB/s", "frac": None if g_rate is None else g_rate / HBM_PEAK_GBS,
-                   "traffic": g_traffic, "ms": gather_ms,
+                   "traffic": g_traffic, "traffic_provenance": g_prof, "ms": gather_ms,
                    "note": "achieved = traffic (rocprofv3 FETCH_SIZE + WRITE_SIZE per launch beyond L2, "
                            "calibrated on a plain copy; it includes last-level-cache hits, so it bounds "
                            "the DRAM rate from above) / the kernel time measured here",
@@ -330,6 +351,7 @@ def main():
                                                 "many queries select come from the caches, so this rate "
                                                 "is not an HBM rate and may exceed the HBM peak"}}
     if attn_impl == "dense":
+        d_prof = profiled_traffic("gsa_dense_attn", args.config)
         qrows = _abi.dense_block_rows(T)         # query rows per block of gsa_dense_attn
         nqb = (T + qrows - 1) // qrows
         dense_flops = 4 * B * H * DH * qrows * 64 * sum(min(qb * qrows + qrows - 1, T - 1) // 64 + 1
@@ -338,7 +360,7 @@ def main():
         ex = dense_flops / (attn_ms * 1e-3) / 1e12
         roofline = {"kernel": "gsa_dense_attn", "bound": "mfma", "achieved": ach, "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": ach / BF16_PEAK_TFLOPS,
-                    "traffic": profiled_traffic("gsa_dense_attn", args.config),
+                    "traffic": (d_prof or {}).get("bytes"), "traffic_provenance": d_prof,
                     "algorithmic_flops": aflops, "executed_flops": dense_flops,
                     "executed_tflops": ex, "executed_frac": ex / BF16_PEAK_TFLOPS, "ms": attn_ms,
                     "note": "achieved/frac: the selected (useful) pairs' QK and PV flops; executed: every "
@@ -370,7 +392,7 @@ def main():
         "gather_attention": gather_roof,
         "indexer": {"kernel": "gsa_indexer_select", "bound": "mfma", "achieved": idx_tflops,
                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": idx_tflops / BF16_PEAK_TFLOPS,
-                    "traffic": profiled_traffic("gsa_indexer_select", args.config),
+                    "traffic": (i_prof or {}).get("bytes"), "traffic_provenance": i_prof,
                     "flops": fidx, "ms": idx_ms},
         "projection": proj,
         "peak_mem_gib": peak_mem / 2**30,

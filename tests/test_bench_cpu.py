@@ -1,6 +1,7 @@
 """bench.py's contract pieces that run without a GPU: more than one GPU is refused
 with a message, and the HBM traffic of the roofline objects comes from the committed
-rocprofv3 summaries (one `traffic_bytes <kernel> <config> <bytes>` line each)."""
+rocprofv3 summaries (one `traffic_bytes <kernel> <config> <bytes> [src=<file>@<sha12>]`
+line each), with the kernel source digest the counters were taken on."""
 
 import os
 import subprocess
@@ -34,7 +35,13 @@ def test_profiled_traffic_lines():
     # reads q_I, k_I, w (10 MiB) and writes the 32 MiB bitmask, storing no score
     # (a stored causal score matrix alone would be 537 MB); the gather kernel misses
     # L2 on most of its 258 GB of gathered rows
-    assert dense is not None and 0.5e9 < dense < 5e9
-    assert idx is not None and 0.044e9 < idx < 0.537e9
-    assert gather is not None and 1e11 < gather < 3e11
+    assert dense is not None and 0.5e9 < dense["bytes"] < 5e9
+    assert idx is not None and 0.044e9 < idx["bytes"] < 0.537e9
+    assert gather is not None and 1e11 < gather["bytes"] < 3e11
     assert bench.profiled_traffic("gsa_dense_attn", "c9") is None
+    # every figure names the summary it came from and the kernel source digest it
+    # was measured on; source_matches compares that digest with today's file
+    for prof, kernel in ((dense, "gsa_dense_attn"), (idx, "gsa_indexer_select"), (gather, "gsa_sparse_attn")):
+        assert prof["source"].startswith("profiles/") and os.path.exists(os.path.join(ROOT, prof["source"]))
+        assert prof["kernel_source"] == f"{bench.KERNEL_SOURCES[kernel]}@{bench.source_digest(kernel)}"
+        assert prof["source_matches"] == (prof["measured_on_source"] == prof["kernel_source"])
