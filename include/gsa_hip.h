@@ -318,7 +318,8 @@ int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel
  * of mask operands per 32 query rows and 64 keys), overwritten by each call
  * -- or, with GSA_ATTN_MASKS_READY, the mask operands gsa_dense_lane_masks
  * wrote there for the same bits, B, T, Tkv and causal (then bits is not
- * read).  bf16 only; d == 128, 1 <= H <= 64.
+ * read).  bf16 only; d == 128, 1 <= H <= 64; row strides k_st, q_st, out_st and
+ * (with their flags) o_st and cs_st at most 2^24 elements, else GSA_ERR_SHAPE.
  */
 size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
 

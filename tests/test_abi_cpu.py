@@ -229,6 +229,11 @@ def test_dense_path_validation(lib):
     assert call(ldv=32) == 2                      # rows shorter than ceil(Tkv/64)*64
     assert call(flags=8) == 6                     # unknown flag
     assert call(bst=3) == 4
+    # row strides past 2^24 elements: the staging tiles' 32-row offsets are 32-bit
+    big = (1 << 24) + 8
+    assert call(qst=big) == 2 and call(outst=big) == 2
+    assert call(ost=big) == 2 and call(ost=big, flags=1, og=None) != 2     # o_st matters only with the gate
+    assert call(cst=big) == 2 and call(cst=big, flags=2) != 2               # cs_st only with RoPE(q)
     lmk = lib.gsa_dense_lane_masks
     assert lmk(None, 0, 2, 1, 4, 4, 1, P, 8 * 1024, None) == 1
     assert lmk(P, 0, 2, 1, 4, 4, 1, None, 8 * 1024, None) == 1

@@ -479,6 +479,47 @@ def test_dense_attention_vs_oracle_and_gather(dev, B, T, H, k):
         assert rel < 5e-3
 
 
+@pytest.mark.parametrize("flags", [0, 1, 2, 3])
+def test_dense_attention_flags_and_strided_rows(dev, flags):
+    """Every combination of RoPE(q) and the output gate, with q, og and out as
+    row-strided views (row stride H*128 + 64 elements, like the layer's views of
+    its fused projection) and T = 300 (the last 32-row wave of the second query
+    block is partly past T): the staged prologue and epilogue read and write
+    exactly the rows and columns of the views, and the result matches the
+    float64 oracle within the bound of the test above; the padding columns
+    beside out's rows stay untouched."""
+    B, T, H, k = 2, 300, 3, 100
+    fl = (_abi.ATTN_ROPE_Q if flags & 1 else 0) | (_abi.ATTN_OUT_GATE if flags & 2 else 0)
+    _log(f"dense_attn flags={fl} strided rows B={B} T={T} H={H} k={k}")
+    q, kk, v, og, ia, cnt = _dense_case(B, T, H, k, seed=31 + flags)
+    cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
+    HD = H * 128
+
+    def strided(x):
+        buf = torch.full((B, T, HD + 64), 7.0, dtype=torch.bfloat16, device=dev)
+        buf[..., :HD] = x.reshape(B, T, HD).to(dev)
+        return buf, buf[..., :HD].view(B, T, H, 128)
+
+    _, qv = strided(q)
+    _, ogv = strided(og)
+    obuf, outv = strided(torch.zeros(B, T, H, 128, dtype=torch.bfloat16))
+    assert qv.stride(1) == HD + 64 and not qv.is_contiguous()
+    vt = torch.zeros(B, H, 128, _abi.vt_len(T), dtype=torch.bfloat16, device=dev)
+    vt[..., :T] = v.to(dev).permute(0, 2, 3, 1)
+    bits = _abi.selection_mask(ia.to(dev), T, count=cnt.to(dev))
+    _abi.dense_attn(qv, kk.to(dev), vt, bits, 128 ** -0.5, og=ogv if fl & _abi.ATTN_OUT_GATE else None,
+                    cos=cos.to(dev), sin=sin.to(dev), flags=fl, out=outv)
+    out = outv.cpu()
+    qr = orc.apply_rope(q, cos[None, :, None], sin[None, :, None]) if fl & _abi.ATTN_ROPE_Q else q
+    mask = torch.arange(k)[None, None, :] < cnt[..., None]
+    att = orc.sparse_attention(qr.double(), kk.double(), v.double(), ia, mask, 128 ** -0.5).to(torch.bfloat16)
+    ref = (att * torch.sigmoid(og) if fl & _abi.ATTN_OUT_GATE else att).double()
+    diff = (out.double() - ref).abs()
+    _log(f"  max|diff| {diff.max().item():.2e}")
+    assert torch.all(diff <= ref.abs() * 2 ** -6 + 2 ** -8 * v.abs().max().item() + 1e-6)
+    assert torch.all(obuf[..., HD:].cpu() == 7.0)
+
+
 @pytest.mark.parametrize("slope", [12.0, -12.0])
 def test_dense_attention_moving_softmax_reference(dev, slope):
     """Logits that climb (or fall) by about `slope` log2 units per 64-key tile.
