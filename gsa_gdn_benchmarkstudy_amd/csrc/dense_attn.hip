@@ -345,6 +345,11 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(w);
   const int i32 = lane & 31, h = lane >> 5;
+  // The wave's 32-row group within the block: waves w and w+4 (one SIMD)
+  // take groups w and 7-w, so that in a causal block each SIMD's two waves
+  // skip the same number of key tiles past their rows (3 + 0, 3 + 0, 2 + 1,
+  // 2 + 1).  Loads into LDS and the staging tile stay indexed by the wave.
+  const int gw = wu < 4 ? wu : 11 - wu;
   // Block order: batch by batch (the blocks in flight then share one
   // sequence's K and V^T, which stays in the last-level cache), within a
   // sequence the heaviest query blocks first, heads fastest.
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
   const uint32_t vdst = lds0 + (uint32_t)(2 * kKU * 16) + (uint32_t)wu * 1024u;
   const uint32_t mdst = lds0 + (uint32_t)(kMBase * 16) + (uint32_t)wu * 1024u;   // + slot * kDW KiB
   // this wave's mask operands: group kDW*qb + w, 1 KiB per tile
-  const char* mbase = reinterpret_cast<const char*>(lm + ((int64_t)b * p.G + kDW * qb + wu) * p.NT * 64);
+  const char* mbase = reinterpret_cast<const char*>(lm + ((int64_t)b * p.G + kDW * qb + gw) * p.NT * 64);
   const uint32_t moff = (uint32_t)lane * 16u;
   auto issue_k = [&](const char* src, int slot, bool last) {   // one K tile into K slot `slot`
 #pragma unroll
@@ -418,14 +423,14 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
   // per instruction keeps every load to 8 cache lines; a lane-per-row load
   // of the same data touches 32 lines per instruction, and a block's
   // prologue then waited several microseconds for its q, cos and sin.
-  const int rbase = min(q0 + 32 * wu, p.T - 1);
+  const int rbase = min(q0 + 32 * gw, p.T - 1);
   const uint32_t xdst = lds0 + (uint32_t)((kXBase + wu * 512) * 16);
   const u32x4* xt = dsm + kXBase + wu * 512;
   auto stage = [&](const uint16_t* base, int64_t row_st) {   // base: element (rbase, column offset)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int r = 4 * j + (lane >> 4);
-      const uint32_t roff = (uint32_t)(min(q0 + 32 * wu + r, p.T - 1) - rbase);
+      const uint32_t roff = (uint32_t)(min(q0 + 32 * gw + r, p.T - 1) - rbase);
       load_lds16(base, roff * (uint32_t)(row_st * 2) + (uint32_t)(((lane & 15) ^ (r & 15)) * 16),
                  xdst + (uint32_t)(j * 1024));
     }
@@ -623,6 +628,8 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
 
   // S^T of tile kt in sc[kt & 1]: with the loop unrolled by two, each
   // iteration writes the other pair, so no accumulator is copied
+  // key tiles this wave computes: up to its last row when causal (uniform)
+  const int nkw_t = (p.flags & kDenseCausal) ? min(nkt, min(p.Tkv - 1, q0 + 32 * gw + 31) / kDK + 1) : nkt;
   floatx16 sc[2][2];
   {
     const intx8 mop = mask_op(0);
@@ -630,13 +637,11 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
     sc[0][1] = s_half(0, 1, mop);                 // S^T of tile 0
   }
   const char* ksrc = kbase + 2 * kstep;            // K tile kt+2
-  // one iteration; P = kt & 1
-  auto step = [&](int kt, auto par) {
-    constexpr int P = decltype(par)::value;
-    // this wave's loads of K(kt+1), its mask operands and V^T(kt) (issued
-    // last iteration) are done and its LDS reads have returned; the
-    // barrier publishes every wave's loads and frees K and mask slot P and
-    // V slot 1-P
+  // Iteration kt, first half: this wave's loads of K(kt+1), its mask
+  // operands and V^T(kt) (issued last iteration) are done and its LDS reads
+  // have returned; the barrier publishes every wave's loads and frees K and
+  // mask slot P = kt & 1 and V slot 1-P for the next loads.
+  auto sync_issue = [&](int kt, int P) {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (kt + 2 < nkt) {
       issue_k(ksrc, P, kt + 3 == nkt);
@@ -648,8 +653,12 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
     // the output-gate rows into the staging tile (free since the q and RoPE
     // reads before the first barrier), awaited at the next barrier
     if (kt == 0 && (p.flags & GSA_ATTN_OUT_GATE)) stage(p.og + b * p.o_sb + (int64_t)rbase * p.o_st + hd * 128, p.o_st);
-
-    // S^T(kt+1) || softmax(kt); stale on the last tile, unused
+  };
+  // One iteration: S^T(kt+1) (stale on the wave's last tile, unused) ||
+  // softmax(kt), then PV(kt).
+  auto step = [&](int kt, auto par) {
+    constexpr int P = decltype(par)::value;
+    sync_issue(kt, P);
     const intx8 mop = mask_op(1 - P);
     sc[1 - P][0] = s_half(1 - P, 0, mop);
     const float mx0 = max_half(sc[P][0]);
@@ -657,12 +666,20 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
     const float mx1 = max_half(sc[P][1]);
     softmax_pv(P, mx0, mx1, sc[P][0], sc[P][1]);
   };
+  // Tiles 0 .. nkw_t-1 with their products (unrolled by two so that slot
+  // offsets are constants), then the block's remaining tiles -- past this
+  // wave's last row when causal: they hold no selected key of its rows, so
+  // their products would add exact zeros -- with the loads and barriers only.
   int t = 0;
-  for (; t + 1 < nkt; t += 2) {
+  for (; t + 1 < nkw_t; t += 2) {
     step(t, Int<0>{});
     step(t + 1, Int<1>{});
   }
-  if (t < nkt) step(t, Int<0>{});
+  if (t < nkw_t) {
+    step(t, Int<0>{});
+    ++t;
+  }
+  for (; t < nkt; ++t) sync_issue(t, t & 1);
 
   // ---- epilogue: normalise, bf16, optional output gate ----
   l = sum_halves(l);
@@ -696,7 +713,7 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
   uint16_t* const ob = p.out + b * p.out_sb + hd * 128;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int r = 4 * j + (lane >> 4), row = q0 + 32 * wu + r;
+    const int r = 4 * j + (lane >> 4), row = q0 + 32 * gw + r;
     const u32x4 v = xt[r * 16 + (lane & 15)];
     if (row < p.T)
       *reinterpret_cast<u32x4*>(ob + (int64_t)row * p.out_st + (((lane & 15) ^ (r & 15)) * 8)) = v;
