@@ -29,6 +29,7 @@ TOPK_DESC_MAX_K = 4096
 ATTN_ROPE_Q = 1
 ATTN_OUT_GATE = 2
 ATTN_MASKS_READY = 4
+ATTN_ROPE_HALVES = 8
 
 # Every symbol include/gsa_hip.h declares.
 EXPORTS = (
@@ -645,7 +646,13 @@ def dense_attn(q, k, vt, bits, scale: float, og=None, cos=None, sin=None, flags:
             "unwritten) and cannot serve a non-causal call")
     if og is not None:
         _expect(tuple(og.shape) == (B, T, H, d) and og.dtype == q.dtype, "og: [B,T,H,d] in q's dtype")
-    if flags & ATTN_ROPE_Q:
+    _expect(not (flags & ATTN_ROPE_HALVES) or flags & ATTN_ROPE_Q, "ATTN_ROPE_HALVES goes with ATTN_ROPE_Q")
+    if flags & ATTN_ROPE_HALVES:
+        # cos: packed [>=T, d] rows of cos[:d/2] then sin[:d/2]; sin is not read
+        _expect(cos is not None and cos.dim() == 2 and cos.shape[0] >= T and cos.shape[1] == d
+                and cos.dtype == q.dtype and cos.stride(1) == 1, "cos: packed [>=T, d] cos|sin table in q's dtype")
+        sin = None
+    elif flags & ATTN_ROPE_Q:
         _expect(cos is not None and sin is not None and cos.dim() == 2 and cos.shape[0] >= T
                 and cos.shape[1] == d and tuple(sin.shape) == tuple(cos.shape)
                 and cos.dtype == sin.dtype == q.dtype and cos.stride(1) == 1 and sin.stride() == cos.stride(),

@@ -11,7 +11,9 @@ min(1, k/(t+1)), k = 2048 by default.  The lane masks are built once per
 library and are not part of the timed region.
 
 Naming a library twice (A B A B) shows the box-to-box and run-to-run spread
-beside the difference.  Each line reports the best of three timed runs of
+beside the difference.  ``--rope halves`` passes RoPE as the packed cos|sin
+table (ATTN_ROPE_HALVES), ``--rope both`` times each library with the full
+tables and then with the packed one.  Each line reports the best of three timed runs of
 `--iters` launches between two HIP events.  This is a tool for kernel work:
 a copy of dense_attn.hip with a change is built into its own library
 (`python -m gsa_gdn_benchmarkstudy_amd.build --dense-src COPY --out LIB`) and
@@ -63,6 +65,8 @@ def main(argv=None) -> int:
     ap.add_argument("--k", type=int, default=2048)
     ap.add_argument("--iters", type=int, default=0, help="launches per timed run (default: 10, 3 past 16K keys)")
     ap.add_argument("--seed", type=int, default=5)
+    ap.add_argument("--rope", choices=("full", "halves", "both"), default="full",
+                    help="RoPE tables: full cos and sin, the packed cos|sin halves, or each in turn")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("attn_ab needs a GPU", file=sys.stderr)
@@ -70,17 +74,25 @@ def main(argv=None) -> int:
     dev = torch.device("cuda:0")
     T = args.T
     q, kk, og, vt, bits, cos, sin = synthetic_inputs(args.B, T, args.H, args.k, args.seed, dev)
+    # RoPE tables whose entries d and d+64 repeat (as RotaryEmbedding builds them), and their packed form
+    cos = torch.cat((cos[:, :64], cos[:, :64]), dim=-1).contiguous()
+    sin = torch.cat((sin[:, :64], sin[:, :64]), dim=-1).contiguous()
+    packed = torch.cat((cos[:, :64], sin[:, :64]), dim=-1).contiguous()
     flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
     scale = 128 ** -0.5
     iters = args.iters or (10 if T <= 16384 else 3)
+    modes = {"full": [False], "halves": [True], "both": [False, True]}[args.rope]
     ref = None
-    for path in args.libs:
+    for path, halves in [(p, h) for p in args.libs for h in modes]:
         _abi._lib = None
         _abi.LIB_PATH = path
         _abi.load()
         ws = _abi.dense_lane_masks(bits, T, causal=True)
 
         def run(out=None):
+            if halves:
+                return _abi.dense_attn(q, kk, vt, bits, scale, og=og, cos=packed, flags=flags | _abi.ATTN_ROPE_HALVES,
+                                       ws=ws, masks_ready=True, out=out)
             return _abi.dense_attn(q, kk, vt, bits, scale, og=og, cos=cos, sin=sin, flags=flags, ws=ws,
                                    masks_ready=True, out=out)
 
@@ -104,7 +116,8 @@ def main(argv=None) -> int:
             e1.record()
             torch.cuda.synchronize()
             runs.append(e0.elapsed_time(e1) / iters)
-        print(f"B={args.B} T={T} {path}: {min(runs):.4f} ms (runs {', '.join(f'{x:.4f}' for x in runs)}), {same}",
+        tag = " (packed cos|sin)" if halves else ""
+        print(f"B={args.B} T={T} {path}{tag}: {min(runs):.4f} ms (runs {', '.join(f'{x:.4f}' for x in runs)}), {same}",
               flush=True)
         del ws, out
     return 0

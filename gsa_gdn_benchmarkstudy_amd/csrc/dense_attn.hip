@@ -454,18 +454,28 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
 #pragma unroll
   for (int s = 0; s < 8; ++s) qraw[s] = xt[xs_unit(i32, 2 * s + h)];
   if (p.flags & GSA_ATTN_ROPE_Q) {
-    // the cos and sin rows through the same tile, after the q reads returned
+    // the cos and sin rows through the same tile, after the q reads returned:
+    // one round for a packed table (row: cos[0:64] then sin[0:64]; entries d
+    // and d+64 are equal), else cos, then sin
     u32x4 craw[8], sraw[8];
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     stage(p.cos + (int64_t)rbase * p.cs_st, p.cs_st);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (p.flags & GSA_ATTN_ROPE_HALVES) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) craw[s] = xt[xs_unit(i32, 2 * s + h)];
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    stage(p.sin + (int64_t)rbase * p.cs_st, p.cs_st);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      for (int s = 0; s < 4; ++s) {
+        craw[s] = craw[s + 4] = xt[xs_unit(i32, 2 * s + h)];
+        sraw[s] = sraw[s + 4] = xt[xs_unit(i32, 8 + 2 * s + h)];
+      }
+    } else {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) sraw[s] = xt[xs_unit(i32, 2 * s + h)];
+      for (int s = 0; s < 8; ++s) craw[s] = xt[xs_unit(i32, 2 * s + h)];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      stage(p.sin + (int64_t)rbase * p.cs_st, p.cs_st);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int s = 0; s < 8; ++s) sraw[s] = xt[xs_unit(i32, 2 * s + h)];
+    }
     auto unpack8 = [](const u32x4& v, float (&x)[8]) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) { x[2 * i] = bf16lo(v[i]); x[2 * i + 1] = bf16hi(v[i]); }
@@ -880,8 +890,11 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
                               void* stream) {
   const bool ready = (flags & GSA_ATTN_MASKS_READY) != 0;
   if (!q || !k || !vt || !out || !ws || (!ready && !bits)) return GSA_ERR_NULL;
-  if (flags & ~(GSA_ATTN_ROPE_Q | GSA_ATTN_OUT_GATE | GSA_ATTN_MASKS_READY)) return GSA_ERR_FLAGS;
-  if ((flags & GSA_ATTN_ROPE_Q) && (!cos || !sin)) return GSA_ERR_NULL;
+  if (flags & ~(GSA_ATTN_ROPE_Q | GSA_ATTN_OUT_GATE | GSA_ATTN_MASKS_READY | GSA_ATTN_ROPE_HALVES))
+    return GSA_ERR_FLAGS;
+  if ((flags & GSA_ATTN_ROPE_HALVES) && !(flags & GSA_ATTN_ROPE_Q)) return GSA_ERR_FLAGS;
+  const bool halves = (flags & GSA_ATTN_ROPE_HALVES) != 0;
+  if ((flags & GSA_ATTN_ROPE_Q) && (!cos || (!halves && !sin))) return GSA_ERR_NULL;
   if ((flags & GSA_ATTN_OUT_GATE) && !og) return GSA_ERR_NULL;
   if (dtype != GSA_DTYPE_BF16) return GSA_ERR_DTYPE;
   if (B < 1 || T < 1 || Tkv < 1 || d != 128 || H < 1 || H > 64) return GSA_ERR_SHAPE;
@@ -902,7 +915,7 @@ extern "C" int gsa_dense_attn(const void* q, int64_t q_sb, int64_t q_st,
       !vec_ok(out, out_sb, out_st, dtype) || !aligned(ws, 16))
     return GSA_ERR_ALIGN;
   if ((flags & GSA_ATTN_OUT_GATE) && !vec_ok(og, o_sb, o_st, dtype)) return GSA_ERR_ALIGN;
-  if ((flags & GSA_ATTN_ROPE_Q) && (!vec_ok(cos, 0, cs_st, dtype) || !vec_ok(sin, 0, cs_st, dtype)))
+  if ((flags & GSA_ATTN_ROPE_Q) && (!vec_ok(cos, 0, cs_st, dtype) || (!halves && !vec_ok(sin, 0, cs_st, dtype))))
     return GSA_ERR_ALIGN;
   if (!ready) {
     const int st = lane_mask_checks(bits, b_sb, b_st, B, T, Tkv, ws, ws_bytes);

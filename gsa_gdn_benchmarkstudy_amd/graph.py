@@ -55,7 +55,8 @@ class GraphedForward:
             self.static_y = model(self.static_x)
         # what the recorded kernels read by address, kept alive by these references
         cast = model.rotary_emb._cast
-        self._tables = (cast[1], cast[2])
+        halves = getattr(model.rotary_emb, "_halves", None)
+        self._tables = (cast[1], cast[2], halves[1] if halves is not None else None)
         self._weights = self._weight_buffers()
         self._cache = self._rope_cache()
 

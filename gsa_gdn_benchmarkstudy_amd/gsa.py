@@ -149,6 +149,25 @@ class RotaryEmbedding(nn.Module):
         self._cast = (key, cos, sin)
         return cos, sin
 
+    def halves(self, seq_len: int, device: torch.device,
+               dtype: Optional[torch.dtype] = None) -> Optional[torch.Tensor]:
+        """The cast tables of ``forward`` packed for the dense attention's RoPE
+        (``ATTN_ROPE_HALVES``): row t holds cos[t][:dim/2] then sin[t][:dim/2].
+        The tables repeat their first half (the angles are cat(freqs, freqs)),
+        so nothing is lost; None when they do not (a cache edited by hand).
+        Kept, like the cast tables, while the cache is unchanged."""
+        cos, sin = self.forward(seq_len, device, dtype)
+        key = self._cast[0]
+        hit = getattr(self, "_halves", None)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        h = self.dim // 2
+        t = None
+        if torch.equal(cos[:, :h], cos[:, h:]) and torch.equal(sin[:, :h], sin[:, h:]):
+            t = torch.cat((cos[:, :h], sin[:, :h]), dim=-1).contiguous()
+        self._halves = (key, t)
+        return t
+
 
 # ---------------------------------------------------------------------------
 # Sub-modules with the reference's state_dict keys (gsa_opt.py:432-507)
@@ -617,8 +636,15 @@ class GatedSparseAttention(nn.Module):
             ev[0].record(cur)
         flags = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
         if dense:
-            attn = _abi.dense_attn(views["q"], k_rope, v_gated, bits, self.scale, og=views["og"],
-                                   cos=cos, sin=sin, flags=flags, causal=True, ws=lm_ws, masks_ready=True)
+            # one table load per block instead of two: cos and sin halves packed
+            cs = self.rotary_emb.halves(T, dev, x.dtype)
+            if cs is not None:
+                attn = _abi.dense_attn(views["q"], k_rope, v_gated, bits, self.scale, og=views["og"],
+                                       cos=cs, flags=flags | _abi.ATTN_ROPE_HALVES, causal=True, ws=lm_ws,
+                                       masks_ready=True)
+            else:
+                attn = _abi.dense_attn(views["q"], k_rope, v_gated, bits, self.scale, og=views["og"],
+                                       cos=cos, sin=sin, flags=flags, causal=True, ws=lm_ws, masks_ready=True)
         else:
             attn = _abi.sparse_attn(views["q"], k_rope, v_gated, idx, self.scale, count=cnt,
                                     og=views["og"], cos=cos, sin=sin, flags=flags)

@@ -59,6 +59,7 @@ extern "C" {
 #define GSA_ATTN_ROPE_Q   1  /* q is pre-RoPE: apply RoPE with cos/sin in the prologue  */
 #define GSA_ATTN_OUT_GATE 2  /* multiply the output by sigmoid(og) (the G1 output gate) */
 #define GSA_ATTN_MASKS_READY 4  /* gsa_dense_attn: ws already holds gsa_dense_lane_masks of bits */
+#define GSA_ATTN_ROPE_HALVES 8  /* gsa_dense_attn with GSA_ATTN_ROPE_Q: cos is the packed table below */
 
 /* Largest k_eff of gsa_topk_select in GSA_ORDER_SCORE_DESC order. */
 #define GSA_TOPK_DESC_MAX_K 4096
@@ -320,6 +321,12 @@ int gsa_selection_mask(const int32_t* idx, int64_t i_sb, int64_t i_st, int k_sel
  * wrote there for the same bits, B, T, Tkv and causal (then bits is not
  * read).  bf16 only; d == 128, 1 <= H <= 64; row strides k_st, q_st, out_st and
  * (with their flags) o_st and cs_st at most 2^24 elements, else GSA_ERR_SHAPE.
+ * GSA_ATTN_ROPE_HALVES (with GSA_ATTN_ROPE_Q): cos points to a packed table
+ * whose row t holds cos[t][0:64] then sin[t][0:64] (128 elements, row stride
+ * cs_st) and sin is not read.  It serves tables whose entries d and d+64 are
+ * equal, as RotaryEmbedding builds them (cat(freqs, freqs),
+ * gsa_triton/gsa_ref.py:52-56; gsa_opt.py:404-429); the output is then
+ * bit-identical to the call with the full cos and sin tables.
  */
 size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
 

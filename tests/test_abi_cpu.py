@@ -45,8 +45,8 @@ def test_constants_match_header(lib):
     assert lib.gsa_abi_version() == m["GSA_ABI_VERSION"] == _abi.ABI_VERSION
     assert (m["GSA_DTYPE_F32"], m["GSA_DTYPE_BF16"]) == (_abi.DTYPE_F32, _abi.DTYPE_BF16)
     assert (m["GSA_ORDER_INDEX_ASC"], m["GSA_ORDER_SCORE_DESC"]) == (_abi.ORDER_INDEX_ASC, _abi.ORDER_SCORE_DESC)
-    assert (m["GSA_ATTN_ROPE_Q"], m["GSA_ATTN_OUT_GATE"], m["GSA_ATTN_MASKS_READY"]) == (
-        _abi.ATTN_ROPE_Q, _abi.ATTN_OUT_GATE, _abi.ATTN_MASKS_READY)
+    assert (m["GSA_ATTN_ROPE_Q"], m["GSA_ATTN_OUT_GATE"], m["GSA_ATTN_MASKS_READY"], m["GSA_ATTN_ROPE_HALVES"]) == (
+        _abi.ATTN_ROPE_Q, _abi.ATTN_OUT_GATE, _abi.ATTN_MASKS_READY, _abi.ATTN_ROPE_HALVES)
     assert m["GSA_TOPK_DESC_MAX_K"] == _abi.TOPK_DESC_MAX_K
 
 
@@ -227,7 +227,11 @@ def test_dense_path_validation(lib):
     assert call(wsb=8 * 1024 - 1) == 2            # workspace too small
     assert call(dtype=0) == 3                     # bf16 only
     assert call(ldv=32) == 2                      # rows shorter than ceil(Tkv/64)*64
-    assert call(flags=8) == 6                     # unknown flag
+    assert call(flags=16) == 6                    # unknown flag
+    assert call(flags=8) == 6 and call(flags=10) == 6   # packed RoPE table without RoPE(q)
+    assert call(flags=1, sin=None) == 1           # RoPE(q) reads sin ...
+    assert call(flags=9, sin=None, wsb=1) == 2    # ... except from the packed table (then the size check fails)
+    assert call(flags=9, cos=None) == 1
     assert call(bst=3) == 4
     # row strides past 2^24 elements: the staging tiles' 32-row offsets are 32-bit
     big = (1 << 24) + 8

@@ -520,6 +520,34 @@ def test_dense_attention_flags_and_strided_rows(dev, flags):
     assert torch.all(obuf[..., HD:].cpu() == 7.0)
 
 
+def test_dense_attention_packed_rope_table(dev):
+    """ATTN_ROPE_HALVES: the cos|sin halves packed into one table (here a
+    row-strided view, row stride 192 elements) give the same bits as the full
+    cos and sin tables, which repeat their first 64 entries as RotaryEmbedding
+    builds them; T = 300 leaves the second query block's last wave partly past
+    T, where the staging tile's rows are clamped."""
+    B, T, H, k = 2, 300, 3, 100
+    _log(f"dense_attn packed RoPE table B={B} T={T} H={H} k={k}")
+    q, kk, v, og, ia, cnt = _dense_case(B, T, H, k, seed=41)
+    cos, sin = orc.RopeCache(128, torch.bfloat16).tables(T, torch.bfloat16)
+    assert torch.equal(cos[:, :64], cos[:, 64:]) and torch.equal(sin[:, :64], sin[:, 64:])
+    buf = torch.full((T, 192), 9.0, dtype=torch.bfloat16)
+    buf[:, :64], buf[:, 64:128] = cos[:, :64], sin[:, :64]
+    packed = buf.to(dev)[:, :128]
+    assert packed.stride(0) == 192
+    vt = torch.zeros(B, H, 128, _abi.vt_len(T), dtype=torch.bfloat16, device=dev)
+    vt[..., :T] = v.to(dev).permute(0, 2, 3, 1)
+    bits = _abi.selection_mask(ia.to(dev), T, count=cnt.to(dev))
+    fl = _abi.ATTN_ROPE_Q | _abi.ATTN_OUT_GATE
+    qd, kd, ogd = q.to(dev), kk.to(dev), og.to(dev)
+    full = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, og=ogd, cos=cos.to(dev), sin=sin.to(dev), flags=fl)
+    half = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, og=ogd, cos=packed, flags=fl | _abi.ATTN_ROPE_HALVES)
+    assert torch.equal(full, half)
+    # and RoPE is really applied: without it the output differs
+    plain = _abi.dense_attn(qd, kd, vt, bits, 128 ** -0.5, og=ogd, flags=_abi.ATTN_OUT_GATE)
+    assert not torch.equal(plain, half)
+
+
 @pytest.mark.parametrize("slope", [12.0, -12.0])
 def test_dense_attention_moving_softmax_reference(dev, slope):
     """Logits that climb (or fall) by about `slope` log2 units per 64-key tile.

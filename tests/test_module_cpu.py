@@ -70,6 +70,25 @@ def test_rotary_matches_oracle_cache_semantics(dtype):
         assert torch.equal(c, rc_c) and torch.equal(s, rc_s), T
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rotary_halves_packs_the_oracle_tables(dtype):
+    """The packed table of the dense attention's RoPE: row t = cos[t][:64] then
+    sin[t][:64] of the oracle's tables, which repeat their first half (also
+    after the rebuild past 8192 rows); a hand-edited cache that breaks the
+    repetition gives None (the module then passes the full tables)."""
+    rot = RotaryEmbedding(128).to(dtype)
+    rc = orc.RopeCache(128, dtype)
+    for T in (100, 8200):
+        cs = rot.halves(T, torch.device("cpu"), dtype)
+        rc_c, rc_s = rc.tables(T, dtype)
+        assert torch.equal(rc_c[:, :64], rc_c[:, 64:]) and torch.equal(rc_s[:, :64], rc_s[:, 64:])
+        assert cs.shape == (T, 128) and cs.is_contiguous()
+        assert torch.equal(cs[:, :64], rc_c[:, :64]) and torch.equal(cs[:, 64:], rc_s[:, :64]), T
+    assert rot.halves(8200, torch.device("cpu"), dtype) is rot.halves(8200, torch.device("cpu"), dtype)
+    rot.cos_cached[5, 100] += 1.0        # the cache is edited: a new version, no longer symmetric
+    assert rot.halves(8200, torch.device("cpu"), dtype) is None
+
+
 def test_no_cpu_fallback():
     m = _model()
     with pytest.raises(RuntimeError):
