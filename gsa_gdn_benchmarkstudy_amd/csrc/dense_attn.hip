@@ -613,6 +613,12 @@ __global__ __launch_bounds__(64 * kDenseWaves, 1) void dense_attn_kernel(DenseAr
   // loads and any such wait would drain them.
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
+  // The second wave of each SIMD issues first whenever both are ready: the
+  // two waves leave each barrier together, and an even arbitration keeps
+  // them in step (both in their MFMA stretches, then both in their softmax
+  // VALU stretches); with one of them ahead, one wave's softmax runs beside
+  // the other's products.  1-1.5 % faster at T = 16384 than equal priority.
+  if (wu >= 4) __builtin_amdgcn_s_setprio(2);
   const char* vsrc = vtb + kDK * 2;                  // V^T tile kt+1
   // Tile kt once both halves' maxima are taken: the softmax decision, P and
   // O^T += V^T(kt) P^T(kt) from V slot vs.
