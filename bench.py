@@ -200,7 +200,7 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build runs the "
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this package runs the "
               f"GSA forward on a single MI355X; multi-GPU sharding is design-only)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():

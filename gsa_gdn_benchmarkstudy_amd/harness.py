@@ -5,7 +5,7 @@
 The user-facing workflow of the reference's gsa_triton/benchmark.py, on
 rocprofv3 and ROCTx instead of Nsight:
 
-- verify (gsa_triton/benchmark.py:101-145): a reference layer and this build's
+- verify (gsa_triton/benchmark.py:101-145): a reference layer and the HIP
   layer with the same weights and the same input, compared elementwise (max and
   mean |diff|, ``allclose`` at --atol/--rtol).  A mismatch ends the run with exit
   status 1 before any timing.
@@ -25,12 +25,12 @@ rocprofv3 and ROCTx instead of Nsight:
 The reference layer is the caller's: ``--ref`` names a Python file or module
 defining ``GatedSparseAttention`` with the reference constructor and state-dict
 keys (the reference repository's ``gsa_triton/gsa_ref.py`` is one).  Without
-``--ref`` only this build's layer is swept and the verification is skipped, which
+``--ref`` only the HIP layer is swept and the verification is skipped, which
 the output says.
 
 Weights follow the reference harness: the reference layer is built under a fixed
 ``torch.manual_seed`` with its default initialisation and its state dict is
-loaded into this build's layer (strict); ``fuse_projections()`` is called on any
+loaded into the HIP layer (strict); ``fuse_projections()`` is called on any
 layer that has it.  Input x ~ N(0, 1).
 """
 
@@ -261,7 +261,7 @@ def sweep(cls, label: str, points: Sequence[Tuple[int, int, int]], device, dtype
     """Time ``cls`` at every (B, T, D) point (gsa_triton/benchmark.py:150-222).
 
     graph: time replays of a HIP graph of the forward (GraphedForward) instead of
-    eager forwards (this build's layer only)."""
+    eager forwards (the HIP layer only)."""
     out(f"\n{'=' * 60}\n  {label}\n{'=' * 60}")
     out(f"{'B':<5} {'T':<7} {'D':<6} | {'ms':>9} | {'tok/s':>14} | {'MB':>9}")
     out("-" * 60)
@@ -399,7 +399,7 @@ def parse_args(argv: Optional[Sequence[str]] = None) -> argparse.Namespace:
                     "sequence lengths, or open a rocprofv3 capture window.")
     p.add_argument("--ref", default=None,
                    help="Python file or module defining the reference GatedSparseAttention "
-                        "(e.g. gsa_triton/gsa_ref.py); without it only this build is swept")
+                        "(e.g. gsa_triton/gsa_ref.py); without it only the HIP layer is swept")
     p.add_argument("--skip-verify", action="store_true", help="skip numerical verification")
     p.add_argument("--verify-T", type=int, default=512, help="sequence length of the verification")
     p.add_argument("--dtype", choices=["bf16", "fp32"], default="bf16")
@@ -413,9 +413,9 @@ def parse_args(argv: Optional[Sequence[str]] = None) -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=WARMUP_ITERS)
     p.add_argument("--iters", type=int, default=BENCH_ITERS)
     p.add_argument("--attn", choices=["auto", "dense", "gather"], default="auto",
-                   help="attention kernel of this build's layer")
+                   help="attention kernel of the HIP layer")
     p.add_argument("--graph", action="store_true",
-                   help="time HIP-graph replays of this build's forward (one launch per forward)")
+                   help="time HIP-graph replays of the HIP layer's forward (one launch per forward)")
     p.add_argument("--json", default=None, help="also write the results to this JSON file")
     # capture windows: the reference's --profile / --ncu flags, same names
     p.add_argument("--profile", action="store_true",

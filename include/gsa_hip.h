@@ -339,7 +339,7 @@ size_t gsa_dense_attn_workspace_bytes(int B, int T, int Tkv);
  * causal != 0: only the key tiles a causal gsa_dense_attn reads (up to the
  * last row of each query block) are built; such masks serve causal calls
  * only.  causal == 0: every tile (serves both).
- * No counterpart in the reference: part of this build's dense attention.
+ * No counterpart in the reference: part of this library's dense attention.
  */
 int gsa_dense_lane_masks(const uint32_t* bits, int64_t b_sb, int64_t b_st,
                          int B, int T, int Tkv, int causal, void* ws, size_t ws_bytes, void* stream);

@@ -1,8 +1,8 @@
 """CPU restatement of the Gated Sparse Attention forward (the oracle).
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
-checker (or as the timed CPU baseline).  The product path
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only to check
+results against (or as the timed CPU baseline).  The product path
 (``gsa_gdn_benchmarkstudy_amd``) never imports it and fails loudly when its HIP
 library is missing.
 

@@ -1,7 +1,7 @@
 """Layer-level parity on the GPU: the drop-in GatedSparseAttention against the
 oracle and the golden fixtures.
 
-Bars (north star): bf16 outputs within atol 2e-2 / rtol 1e-2 of the oracle,
+Bars: bf16 outputs within atol 2e-2 / rtol 1e-2 of the oracle,
 fp32 within 1e-4; the selected index sets overlap >= 99.9%.  Because GSA
 outputs are ~1e-2 in magnitude, every bf16 test also bounds the relative L2
 error, and the fp32 tests compare against the oracle fed the kernel's own
