@@ -360,9 +360,17 @@ def main():
                                                       for g in range(nqb * qrows // 32))
         ach = aflops / (attn_ms * 1e-3) / 1e12
         ex = dense_flops / (attn_ms * 1e-3) / 1e12
+        d_traffic = (d_prof or {}).get("bytes")
+        d_rate = None if d_traffic is None else d_traffic / (attn_ms * 1e-3) / 1e9
         roofline = {"kernel": "gsa_dense_attn", "bound": "mfma", "achieved": ach, "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": ach / BF16_PEAK_TFLOPS,
-                    "traffic": (d_prof or {}).get("bytes"), "traffic_provenance": d_prof,
+                    "traffic": d_traffic, "traffic_provenance": d_prof,
+                    "hbm_rate": {"value": d_rate, "unit": "GB/s", "peak": HBM_PEAK_GBS,
+                                 "frac": None if d_rate is None else d_rate / HBM_PEAK_GBS,
+                                 "note": "the timed step's attention as an HBM figure: its profiled traffic "
+                                         "beyond L2 (FETCH_SIZE + WRITE_SIZE, calibrated) over the time "
+                                         "measured here; the kernel is MFMA-bound, so this is what it asks "
+                                         "of HBM, not a limit it reaches"},
                     "algorithmic_flops": aflops, "executed_flops": dense_flops,
                     "executed_tflops": ex, "executed_frac": ex / BF16_PEAK_TFLOPS, "ms": attn_ms,
                     "note": "achieved/frac: the selected (useful) pairs' QK and PV flops; executed: the bf16 "
