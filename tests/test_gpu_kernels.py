@@ -351,7 +351,7 @@ def _attn_ref64(q, k, v, idx, mask, scale):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("B,T,H,k", [(1, 64, 16, 16), (2, 37, 4, 37), (1, 300, 2, 100)])
+@pytest.mark.parametrize("B,T,H,k", [(1, 64, 16, 16), (2, 37, 4, 37), (1, 300, 2, 100), (1, 100, 64, 30)])
 def test_sparse_attention_vs_oracle(dev, dtype, B, T, H, k):
     _log(f"sparse_attn dtype={dtype} B={B} T={T} H={H} k={k}")
     q, kk, v, idx, mask = _attn_case(dtype, B, T, H, k, seed=T)
@@ -449,7 +449,10 @@ def _dense_case(B, T, H, k, seed):
                                      # 256-row query blocks and 64-key tiles: one short of, at and
                                      # one past the boundaries; one head; odd batch counts
                                      (1, 255, 1, 64), (3, 256, 2, 32), (1, 257, 1, 256), (2, 513, 2, 100),
-                                     (1, 767, 3, 767)])
+                                     (1, 767, 3, 767),
+                                     # more heads than the layer's 16, up to the ABI's 64 (the grid
+                                     # puts heads fastest; 40 is no power of two)
+                                     (2, 200, 40, 60), (1, 300, 64, 100)])
 def test_dense_attention_vs_oracle_and_gather(dev, B, T, H, k):
     _log(f"dense_attn B={B} T={T} H={H} k={k}")
     q, kk, v, og, ia, cnt = _dense_case(B, T, H, k, seed=T + H)
