@@ -307,15 +307,16 @@ def test_indexer_select_long_rows_T65536(dev):
     assert same / total >= 0.999
 
 
-@pytest.mark.parametrize("dtype,k_scale", [(torch.bfloat16, 1.0), (torch.float32, 1.0),
-                                           (torch.bfloat16, 1e-37), (torch.bfloat16, 1e37)])
-def test_prologue_vs_oracle(dev, dtype, k_scale):
+@pytest.mark.parametrize("dtype,k_scale,H", [(torch.bfloat16, 1.0, 4), (torch.float32, 1.0, 4),
+                                             (torch.bfloat16, 1e-37, 4), (torch.bfloat16, 1e37, 4),
+                                             (torch.bfloat16, 1.0, 64), (torch.float32, 1.0, 64)])
+def test_prologue_vs_oracle(dev, dtype, k_scale, H):
     """RoPE(k) bit-exact with the oracle's bf16 ops (every product and sum rounded to
     bf16, round-to-nearest-even; random bf16 operands hit exact ties about once per
     256 products); k_scale 1e-37 puts the products and sums among fp32 subnormals,
-    1e37 near the top of the range."""
-    B, T, H = 2, 40, 4
-    _log(f"prologue dtype={dtype} k_scale={k_scale}")
+    1e37 near the top of the range; 64 heads: one 1024-thread block per row."""
+    B, T = 2, 40
+    _log(f"prologue dtype={dtype} k_scale={k_scale} H={H}")
     g = torch.Generator().manual_seed(1)
     k = (torch.randn(B, T, H, 128, generator=g) * k_scale).to(dtype)
     v = torch.randn(B, T, H, 128, generator=g).to(dtype)
@@ -402,9 +403,9 @@ def test_sparse_attention_fused_rope_gate_count(dev, dtype):
 # block-dense attention path
 # ---------------------------------------------------------------------------
 
-def test_prologue_vt_matches_prologue(dev):
-    B, T, H = 2, 100, 4
-    _log("prologue_vt")
+@pytest.mark.parametrize("B,T,H", [(2, 100, 4), (1, 130, 64)])
+def test_prologue_vt_matches_prologue(dev, B, T, H):
+    _log(f"prologue_vt B={B} T={T} H={H}")
     g = torch.Generator().manual_seed(11)
     k = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16).to(dev)
     v = torch.randn(B, T, H, 128, generator=g).to(torch.bfloat16).to(dev)
@@ -413,7 +414,7 @@ def test_prologue_vt_matches_prologue(dev):
     cos, sin = cos.to(dev), sin.to(dev)
     ko, vo = _abi.prologue(k=k, v=v, vg=vg, cos=cos, sin=sin)
     ko2, vt = _abi.prologue_vt(v, vg, k=k, cos=cos, sin=sin)
-    assert vt.shape == (B, H, 128, 128)
+    assert vt.shape == (B, H, 128, _abi.vt_len(T))
     assert torch.equal(ko.cpu(), ko2.cpu())
     assert torch.equal(vt[..., :T].cpu(), vo.permute(0, 2, 3, 1).cpu())
     assert torch.all(vt[..., T:].cpu() == 0)
