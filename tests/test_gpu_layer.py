@@ -149,6 +149,21 @@ def test_layer_vs_oracle_small(dev, dtype, impl, B, T):
         _check_bf16(y, orc.gsa_forward(sd, cfg, x))
 
 
+@pytest.mark.parametrize("impl", ["dense", "gather"])
+def test_layer_vs_oracle_32_heads(dev, impl):
+    """A wider layer than the reference's default (D=4096, 32 heads) in bf16: the
+    fused weight, the strided projection views and both attention kernels at twice
+    the head count of the benchmark layer."""
+    _log(f"layer 32 heads impl={impl}")
+    cfg = orc.GSAConfig(hidden_size=4096, num_heads=32, k_max=96, k_base=64, k_min=16)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=17), torch.bfloat16)
+    x = orc.synthetic_input(1, 160, cfg.hidden_size, seed=18).to(torch.bfloat16)
+    m = _model(cfg, sd, dev, torch.bfloat16, impl)
+    with torch.no_grad():
+        y = m(x.to(dev)).cpu()
+    _check_bf16(y, orc.gsa_forward(sd, cfg, x))
+
+
 def test_layer_c1_fp32(dev):
     """The CPU-runnable reference workload: D=2048, H=16, T=512, k_base=256, k_max=512, fp32."""
     _log("layer c1 fp32 T=512")
