@@ -149,6 +149,28 @@ def test_layer_vs_oracle_small(dev, dtype, impl, B, T):
         _check_bf16(y, orc.gsa_forward(sd, cfg, x))
 
 
+@pytest.mark.parametrize("dtype,impl", [(torch.bfloat16, "dense"), (torch.bfloat16, "gather"),
+                                        (torch.float32, "gather")])
+@pytest.mark.parametrize("B,T", [(1, 1), (2, 2), (1, 17)])
+def test_layer_vs_oracle_short(dev, dtype, impl, B, T):
+    """Sequences of 1, 2 and 17 tokens: every row selects its whole causal prefix
+    (k_eff = min(k_base, k_max, T) = T), the attention blocks and key tiles are
+    almost all padding."""
+    _log(f"layer short dtype={dtype} impl={impl} B={B} T={T}")
+    cfg = orc.GSAConfig(hidden_size=512, num_heads=4, k_max=96, k_base=64, k_min=16)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=27), dtype)
+    x = orc.synthetic_input(B, T, cfg.hidden_size, seed=28).to(dtype)
+    m = _model(cfg, sd, dev, dtype, impl)
+    with torch.no_grad():
+        y = m(x.to(dev)).cpu()
+    ref = orc.gsa_forward(sd, cfg, x)
+    assert y.shape == ref.shape
+    if dtype == torch.float32:
+        assert torch.allclose(y, ref, atol=1e-4, rtol=0)
+    else:
+        _check_bf16(y, ref)
+
+
 @pytest.mark.parametrize("impl", ["dense", "gather"])
 def test_layer_vs_oracle_32_heads(dev, impl):
     """A wider layer than the reference's default (D=4096, 32 heads) in bf16: the
