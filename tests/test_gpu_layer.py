@@ -172,6 +172,36 @@ def test_layer_vs_oracle_short(dev, dtype, impl, B, T):
 
 
 @pytest.mark.parametrize("impl", ["dense", "gather"])
+def test_layer_input_views_and_ignored_mask(dev, impl):
+    """The forward takes x as any strided view (a column slice of a wider buffer, a
+    batch-transposed view): each within the bf16 bar of the oracle (the projection
+    GEMM over a strided x may take another hipBLASLt algorithm, whose bf16 results
+    differ from the contiguous call's by an ulp here and there), and ignores
+    attention_mask as the reference does (gsa_opt.py:617-618): the same bits."""
+    _log(f"layer input views impl={impl}")
+    cfg = orc.GSAConfig(hidden_size=512, num_heads=4, k_max=96, k_base=64, k_min=16)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=37), torch.bfloat16)
+    xc = orc.synthetic_input(2, 130, cfg.hidden_size, seed=38).to(torch.bfloat16)
+    ref = orc.gsa_forward(sd, cfg, xc)
+    x = xc.to(dev)
+    m = _model(cfg, sd, dev, torch.bfloat16, impl)
+    with torch.no_grad():
+        y = m(x)
+        _check_bf16(y.cpu(), ref)
+        wide = torch.zeros(2, 130, cfg.hidden_size + 64, dtype=x.dtype, device=dev)
+        wide[..., 32:32 + cfg.hidden_size] = x
+        xs = wide[..., 32:32 + cfg.hidden_size]
+        xt = x.transpose(0, 1).contiguous().transpose(0, 1)
+        assert not xs.is_contiguous() and not xt.is_contiguous()
+        for v in (xs, xt):
+            yv = m(v)
+            assert yv.shape == y.shape and yv.is_contiguous()
+            _check_bf16(yv.cpu(), ref)
+        mask = torch.zeros(2, 1, 130, 130, dtype=torch.bool, device=dev)
+        assert torch.equal(m(x, attention_mask=mask), y)
+
+
+@pytest.mark.parametrize("impl", ["dense", "gather"])
 def test_layer_vs_oracle_32_heads(dev, impl):
     """A wider layer than the reference's default (D=4096, 32 heads) in bf16: the
     fused weight, the strided projection views and both attention kernels at twice
