@@ -278,6 +278,29 @@ def test_layer_repeat_is_deterministic(dev):
     assert torch.equal(a, b)
 
 
+def test_forward_on_a_caller_stream(dev):
+    """Issued on a caller's own stream (the layer's second stream then hangs off that
+    stream, as the reference's side stream hangs off the current one,
+    gsa_opt.py:654-659), every placement gives the default stream's bits, read
+    after synchronising only the caller's stream."""
+    cfg = orc.GSAConfig(hidden_size=512, num_heads=4, k_max=96, k_base=64, k_min=16)
+    sd = orc.cast_state(orc.synthetic_state(cfg, seed=45), torch.bfloat16)
+    x = orc.synthetic_input(2, 300, cfg.hidden_size, seed=46).to(torch.bfloat16).to(dev)
+    m = _model(cfg, sd, dev, torch.bfloat16)
+    with torch.no_grad():
+        ref = m(x)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=dev)
+    for mode in ("gemm", "producer", "serial", "auto"):
+        _log(f"caller stream, placement {mode}")
+        m.indexer_overlap = mode
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.no_grad(), torch.cuda.stream(s):
+            z = m(x).clone()
+        s.synchronize()
+        assert torch.equal(z, ref), mode
+
+
 def test_indexer_overlap_modes_identical(dev):
     """Every stream arrangement of the indexer (beside the GEMM, beside the
     producer, serial with the lane masks in the producer's launch or on a second
